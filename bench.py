@@ -1,0 +1,404 @@
+"""Benchmark of the NF4 hot path on one MI355X.
+
+`value` is the throughput of one FLUX single-stream block's NF4 linears at 1024^2
+(M = 4608 tokens: linear1 3072 -> 21504 and linear2 15360 -> 3072, weights N(0, 0.02)
+NF4 blocksize 64, activations bf16 N(0, 1)), in TFLOP/s, inputs resident in HBM. A
+step is linear1 + linear2 once; weights rotate over 8 distinct copies (512 MB of NF4,
+above the 256 MB Infinity Cache).
+
+The same JSON line carries:
+  roofline      the fused GEMM kernel's FLOP/s from HIP-event durations of its launches
+                against the 2.5 PFLOP/s dense bf16 MFMA peak;
+  cpu_baseline  the reference's dequantize-then-torch path (the oracle's C decode + torch
+                F.linear in fp32) on the host cores, on a bounded row sample;
+  extra         the other configurations: the 1536-token single linear, the 76 hoisted
+                modulation GEMMs at M = 28 (HBM-bound, GB/s), the fused segments at M = 4608
+                (GB/s), the library dequant + hipBLASLt path on the GPU for comparison, and
+                with --full-step the full FLUX-dev-shaped step at 1024^2 (s/step).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--full-step] [--no-extra] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+METRIC = "NF4 linear TFLOP/s & HBM GB/s (% roofline); s/step FLUX 1024² on 1 GPU"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+D, MLP, M_1024 = 3072, 12288, 4608
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def nf4_weight(n, k, seed, dev):
+    from selas_amd import codecs
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = torch.randn(n, k, generator=g, device=dev) * 0.02
+    e = codecs.encode_nf4("w", w)
+    del w
+    return e
+
+
+def bias(n, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(n, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+
+def act(m, k, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+
+
+def lin(x, e, b=None):
+    from selas_amd import codecs
+    from selas_amd.linear import nf4_linear
+
+    return nf4_linear(x, e.parts["packed"], e.parts["absmax"], 64, codecs.NF4_CODE, e.shape, b)
+
+
+class Timer:
+    """HIP events on the current stream around individual launches."""
+
+    def __init__(self):
+        self.pairs: dict[str, list] = {}
+
+    def start(self, name):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return name, e
+
+    def stop(self, tok):
+        name, e0 = tok
+        e1 = torch.cuda.Event(enable_timing=True)
+        e1.record()
+        self.pairs.setdefault(name, []).append((e0, e1))
+
+    def mean_ms(self, name):
+        ps = self.pairs.get(name, [])
+        return sum(a.elapsed_time(b) for a, b in ps) / max(1, len(ps))
+
+
+# --------------------------------------------------------------------------- config 2 (the value)
+
+
+def bench_block_linears(dev, steps, warmup, copies=8):
+    f1 = 2.0 * M_1024 * (3 * D + MLP) * D
+    f2 = 2.0 * M_1024 * D * (D + MLP)
+    w1 = [nf4_weight(3 * D + MLP, D, 100 + i, dev) for i in range(copies)]
+    w2 = [nf4_weight(D, D + MLP, 200 + i, dev) for i in range(copies)]
+    b1, b2 = bias(3 * D + MLP, 1, dev), bias(D, 2, dev)
+    x1, x2 = act(M_1024, D, 2, dev), act(M_1024, D + MLP, 3, dev)
+    for i in range(warmup):
+        lin(x1, w1[i % copies], b1)
+        lin(x2, w2[i % copies], b2)
+    torch.cuda.synchronize(dev)
+    tm = Timer()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        t = tm.start("linear1")
+        lin(x1, w1[i % copies], b1)
+        tm.stop(t)
+        t = tm.start("linear2")
+        lin(x2, w2[i % copies], b2)
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
+    wall = (time.perf_counter() - t0) / steps
+    k1, k2 = tm.mean_ms("linear1"), tm.mean_ms("linear2")
+    nbytes = sum(e.nbytes for e in (w1[0], w2[0]))
+    return {
+        "flop_per_step": f1 + f2, "ms_per_step": wall * 1e3,
+        "kernel_ms": {"linear1": k1, "linear2": k2},
+        "kernel_tflops": {"linear1": f1 / k1 / 1e9, "linear2": f2 / k2 / 1e9},
+        "achieved_tflops": (f1 + f2) / (k1 + k2) / 1e9,
+        "nf4_bytes_per_step": nbytes,
+        "shapes": {"linear1": [M_1024, 3 * D + MLP, D], "linear2": [M_1024, D, D + MLP]},
+    }
+
+
+# --------------------------------------------------------------------------- extras
+
+
+def bench_single_linear(dev, steps, warmup):
+    m, n, k = 1536, 12288, 3072
+    ws = [nf4_weight(n, k, 300 + i, dev) for i in range(8)]
+    x = act(m, k, 1, dev)
+    for i in range(warmup):
+        lin(x, ws[i % 8])
+    torch.cuda.synchronize(dev)
+    tm = Timer()
+    for i in range(steps):
+        t = tm.start("l")
+        lin(x, ws[i % 8])
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
+    ms = tm.mean_ms("l")
+    return {"shape": [m, n, k], "kernel_ms": ms, "tflops": 2.0 * m * n * k / ms / 1e9}
+
+
+def bench_library_path(dev, steps, warmup):
+    """The reference's GPU path for one block's linears: decode to bf16, then F.linear (hipBLASLt)."""
+    from selas_amd import codecs
+
+    w1, w2 = nf4_weight(3 * D + MLP, D, 100, dev), nf4_weight(D, D + MLP, 200, dev)
+    x1, x2 = act(M_1024, D, 2, dev), act(M_1024, D + MLP, 3, dev)
+
+    def run():
+        a = codecs.decode("nf4", w1.parts, w1.meta, w1.shape, torch.bfloat16)
+        torch.nn.functional.linear(x1, a)
+        b = codecs.decode("nf4", w2.parts, w2.meta, w2.shape, torch.bfloat16)
+        torch.nn.functional.linear(x2, b)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize(dev)
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    f = 2.0 * M_1024 * ((3 * D + MLP) * D + D * (D + MLP))
+    # the GEMMs alone on pre-decoded weights
+    a = codecs.decode("nf4", w1.parts, w1.meta, w1.shape, torch.bfloat16)
+    b = codecs.decode("nf4", w2.parts, w2.meta, w2.shape, torch.bfloat16)
+    tm = Timer()
+    for _ in range(steps):
+        t = tm.start("g")
+        torch.nn.functional.linear(x1, a)
+        torch.nn.functional.linear(x2, b)
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
+    g = tm.mean_ms("g")
+    return {"ms_per_step": ms, "tflops": f / ms / 1e9, "gemm_only_ms": g, "gemm_only_tflops": f / g / 1e9}
+
+
+def bench_modulations(dev, steps, warmup):
+    """76 hoisted adaLN linears at M = 28 (19 double blocks x img/txt 3072 -> 18432, 38 single 3072 -> 9216)."""
+    s = 28
+    ws = [nf4_weight(6 * D, D, 400 + i, dev) for i in range(38)] + [nf4_weight(3 * D, D, 500 + i, dev) for i in range(38)]
+    bs = [bias(e.shape[0], 600 + i, dev) for i, e in enumerate(ws)]
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.nn.functional.silu(torch.randn(s, D, generator=g, device=dev)).to(torch.bfloat16)
+    nbytes = sum(e.nbytes for e in ws) + sum(b.numel() * 2 for b in bs) + 76 * s * D * 2 + sum(s * e.shape[0] * 2 for e in ws)
+    flops = sum(2.0 * s * e.shape[0] * D for e in ws)
+
+    def run(tm=None):
+        for e, b in zip(ws, bs):
+            t = tm.start("gemv") if tm else None
+            lin(x, e, b)
+            if tm:
+                tm.stop(t)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize(dev)
+    reps = max(1, steps // 4)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize(dev)
+    wall = (time.perf_counter() - t0) / reps
+    tm = Timer()
+    run(tm)
+    torch.cuda.synchronize(dev)
+    per = tm.mean_ms("gemv")
+    return {"launches": 76, "bytes": nbytes, "flops": flops, "wall_ms": wall * 1e3, "gbs_wall": nbytes / wall / 1e9,
+            "kernel_ms_mean": per, "gbs_kernel": nbytes / (per * 76) / 1e6}
+
+
+def bench_segments(dev, steps, warmup):
+    from selas_amd.kernels import Kernels
+
+    k = Kernels()
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(1, M_1024, D, generator=g, device=dev)
+    mod = torch.randn(1, 3 * D, generator=g, device=dev) * 0.1
+    sh, sc, gate = mod.float().unsqueeze(1).chunk(3, dim=-1)
+    h = torch.randn(1, M_1024, 3 * D + MLP, generator=g, device=dev).to(torch.bfloat16)
+    qkv = h[..., :3 * D]
+    qs = 1 + 0.02 * torch.randn(128, generator=g, device=dev)
+    ks = 1 + 0.02 * torch.randn(128, generator=g, device=dev)
+    ang = torch.rand(M_1024, 64, generator=g, device=dev, dtype=torch.float64) * 50
+    cos, sin = ang.cos().float(), ang.sin().float()
+    y = torch.randn(1, M_1024, D, generator=g, device=dev).to(torch.bfloat16)
+    attn = torch.randn(1, M_1024, D, generator=g, device=dev).to(torch.bfloat16)
+    cases = {
+        # name: (fn, algorithmic bytes per call)
+        "mod_in": (lambda: k.mod_in(x, sh, sc, torch.bfloat16), M_1024 * D * (4 + 2) + 2 * D * 4),
+        "qkv_single": (lambda: k.qkv_single(qkv, qs, ks, cos, sin, 24, torch.bfloat16),
+                       M_1024 * 3 * D * 2 * 2 + 2 * M_1024 * 64 * 4),
+        "gated_add": (lambda: k.gated_add(x, gate, y, False), M_1024 * D * (4 + 2 + 4) + D * 4),
+        "attn_mlp": (lambda: k.attn_mlp(attn, h[..., 3 * D:]), M_1024 * (D + MLP) * 2 * 2),
+    }
+    out = {}
+    for name, (fn, nb) in cases.items():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize(dev)
+        tm = Timer()
+        for _ in range(steps):
+            t = tm.start(name)
+            fn()
+            tm.stop(t)
+        torch.cuda.synchronize(dev)
+        ms = tm.mean_ms(name)
+        out[name] = {"bytes": nb, "kernel_ms": ms, "gbs": nb / ms / 1e6, "frac_hbm": nb / ms / 1e6 / PEAK_HBM_GBS}
+    return out
+
+
+def bench_full_step(dev, steps, warmup):
+    from selas_amd import flux as F
+
+    cfg = F.FluxConfig()
+    t0 = time.perf_counter()
+    model = F.RandomFlux(cfg, dev, torch.bfloat16, seed=0)
+    torch.cuda.synchronize(dev)
+    build_s = time.perf_counter() - t0
+    g = torch.Generator(device=dev).manual_seed(5)
+    n_steps = 28
+    sv = torch.nn.functional.silu(torch.randn(n_steps, 1, D, generator=g, device=dev)).to(torch.bfloat16)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    mods = model.modulations(sv)
+    torch.cuda.synchronize(dev)
+    prologue_s = time.perf_counter() - t0
+    lt, grid = 512, 64
+    txt = torch.randn(1, lt, D, generator=g, device=dev)
+    lat = torch.randn(1, grid * grid, 64, generator=g, device=dev)
+    fmod = (torch.randn(1, 2 * D, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    ids = torch.cat((torch.zeros(lt, 3, device=dev), F.image_ids(grid, grid, dev)), dim=0)
+    cos, sin = F.rope_tables(ids, cfg.axes_dim, cfg.theta)
+    for s in range(warmup):
+        model.step(lat, txt, [m[s] for m in mods], fmod, cos, sin)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        v = model.step(lat, txt, [m[s % n_steps] for m in mods], fmod, cos, sin)
+    torch.cuda.synchronize(dev)
+    step_s = (time.perf_counter() - t0) / steps
+    assert torch.isfinite(v).all()
+    lin_f = sum(F.unit_flops(kd, cfg, grid * grid, lt, 1)[0] * n for kd, n in (("double", 19), ("single", 38)))
+    att_f = sum(F.unit_flops(kd, cfg, grid * grid, lt, 1)[1] * n for kd, n in (("double", 19), ("single", 38)))
+    return {"s_per_step": step_s, "tflops": (lin_f + att_f) / step_s / 1e12, "linear_tflop": lin_f / 1e12,
+            "attention_tflop": att_f / 1e12, "prologue_s": prologue_s, "build_s": build_s,
+            "nf4_resident_gb": model.nf4_bytes() / 1e9}
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(target_s: float = 12.0):
+    """Dequantize-then-F.linear on the host for one block's two linears at M = 4608 (fp32, all cores).
+
+    The weights are decoded by the oracle's C restatement of the reference decode; the GEMM runs on a
+    row sample sized to about `target_s` seconds and the full-step time is extrapolated linearly in rows."""
+    import numpy as np
+
+    from oracle import nf4 as onf4
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(0)
+    shapes = [(3 * D + MLP, D), (D, D + MLP)]
+    dec_s, gemm_s_per_row = 0.0, 0.0
+    rows_used = 0
+    for n, k in shapes:
+        w = (rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+        p, a = onf4.c_encode(w) if onf4.c_lib() else onf4.encode(w)
+        del w
+        t0 = time.perf_counter()
+        wd = onf4.c_decode(p, a, 64) if onf4.c_lib() else onf4.decode(p, a, 64)
+        dec_s += time.perf_counter() - t0
+        wt = torch.from_numpy(wd).view(n, k)
+        rows = 64
+        while True:
+            x = torch.randn(rows, k)
+            t0 = time.perf_counter()
+            torch.nn.functional.linear(x, wt)
+            dt = time.perf_counter() - t0
+            if dt > target_s / 4 or rows >= M_1024:
+                break
+            rows = min(M_1024, rows * 4)
+        gemm_s_per_row += dt / rows
+        rows_used = max(rows_used, rows)
+    step_s = dec_s + gemm_s_per_row * M_1024
+    f = 2.0 * M_1024 * ((3 * D + MLP) * D + D * (D + MLP))
+    return {"value": f / step_s / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"oracle C decode of both weights + torch fp32 F.linear on {rows_used}-row samples, "
+                      f"extrapolated to 4608 rows: {step_s:.2f} s per step ({dec_s:.2f} s decode)"}
+
+
+# --------------------------------------------------------------------------- main
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--full-step", action="store_true", help="also time the full FLUX-dev-shaped step at 1024^2")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    log(f"bench: {torch.cuda.get_device_name(dev)}")
+    res = bench_block_linears(dev, a.steps, a.warmup)
+    log(f"bench: block linears {res['kernel_tflops']}")
+    extra = {"block_linears": res}
+    if not a.no_extra:
+        extra["single_linear_1536"] = bench_single_linear(dev, a.steps, a.warmup)
+        log(f"bench: single linear {extra['single_linear_1536']['tflops']:.1f} TFLOP/s")
+        extra["modulations_m28"] = bench_modulations(dev, a.steps, a.warmup)
+        log(f"bench: modulations {extra['modulations_m28']['gbs_kernel']:.0f} GB/s")
+        extra["segments_m4608"] = bench_segments(dev, a.steps, a.warmup)
+        log(f"bench: segments {json.dumps({k: round(v['gbs']) for k, v in extra['segments_m4608'].items()})}")
+        extra["library_path"] = bench_library_path(dev, a.steps, a.warmup)
+        log(f"bench: library path {extra['library_path']['tflops']:.1f} TFLOP/s")
+    if a.full_step:
+        extra["full_step_1024"] = bench_full_step(dev, max(3, a.steps // 4), 2)
+        log(f"bench: full step {extra['full_step_1024']['s_per_step']:.3f} s")
+    cpu = None if a.no_cpu else cpu_baseline()
+    achieved = res["achieved_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": res["flop_per_step"] / (res["ms_per_step"] / 1e3) / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "FLUX single-stream block NF4 linears at 1024^2: M=4608, linear1 3072->21504 + "
+                               "linear2 15360->3072, NF4 blocksize 64, bf16 activations", "tokens": M_1024,
+                   "hidden": D, "mlp_hidden": MLP, "blocksize": 64, "weight_copies": 8},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,152 @@
+/*
+ * selas_amd.h - C ABI of the MI355X (gfx950) NF4 hot path.
+ *
+ * One shared library, libselas_amd.so, built by hipcc from selas_amd/csrc/.
+ * Every entry point:
+ *   - takes plain device pointers, element counts and strides (in elements,
+ *     not bytes), never a framework type;
+ *   - launches asynchronously on the HIP stream passed as `stream` (a
+ *     hipStream_t; pass the caller's current stream so that stream-ordered
+ *     buffer reuse stays correct) and never synchronises the device;
+ *   - allocates nothing and frees nothing: outputs are caller-owned;
+ *   - returns SELAS_OK or an error code and never throws; the message of the
+ *     last error on the calling thread is returned by selas_last_error().
+ *
+ * Data formats follow the reference codec (selas/codecs.py:1-16, 58-63,
+ * 99-119): NF4 weights are `packed` uint8 [numel/2] (element 2i in the high
+ * nibble of byte i), `absmax` fp32 [numel/blocksize] over the flattened
+ * tensor, and a 16-entry fp32 codebook passed by value from host memory
+ * (the tensor's meta["code"]).
+ *
+ * Kernels are chosen from shapes, dtypes and pointer alignment only and use
+ * no atomics, so equal inputs give equal bits on every call.
+ */
+#ifndef SELAS_AMD_H
+#define SELAS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+#define SELAS_OK 0
+#define SELAS_EINVAL 1       /* invalid argument (sizes, dtypes, nulls): ValueError in the reference */
+#define SELAS_EUNSUPPORTED 2 /* valid, but outside what a fused kernel covers: caller falls back */
+#define SELAS_EHIP 3         /* HIP runtime or launch error */
+
+/* Element types (the `dtype` arguments). */
+#define SELAS_F32 0
+#define SELAS_F16 1
+#define SELAS_BF16 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *selas_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int selas_abi_version(void);
+
+/* ------------------------------------------------------------------ codec */
+
+/*
+ * NF4 decode: out[2i]   = dtype(code[packed[i] >> 4] * absmax[i / (blocksize/2)])
+ *             out[2i+1] = dtype(code[packed[i] & 15] * absmax[i / (blocksize/2)])
+ * The fp32 product is rounded once, to nearest even, to out_dtype; the bits
+ * equal the reference decode for every input, NaN included.
+ * Replaces nf4_dequant / nf4_dequant_torch (selas/codecs.py:178-199, 260-266)
+ * and the Triton kernel (codecs.py:207-228).
+ */
+int selas_nf4_dequant(const uint8_t *packed, const float *absmax, int64_t n_bytes, int64_t blocksize,
+                      const float code[16], void *out, int out_dtype, void *stream);
+
+/*
+ * NF4 encode of an fp32 tensor of n elements (n % blocksize == 0, blocksize
+ * even): absmax[b] = max |w| over block b; each element divided by the block's
+ * absmax (1 where absmax is 0) is mapped to the number of codebook midpoints
+ * (code[i]+code[i+1])/2 that are not >= it (ties go to the lower code), and
+ * two codes are packed per byte, first element high.
+ * Replaces encode_nf4 (selas/codecs.py:99-119).
+ */
+int selas_nf4_encode(const float *w, int64_t n, int64_t blocksize, const float code[16], uint8_t *packed,
+                     float *absmax, void *stream);
+
+/* ------------------------------------------------------------ linear */
+
+/*
+ * Quantized linear forward y = x W^T + bias with W an NF4 [N, K] weight:
+ *   x     [M, K]  dtype, row stride ldx (K contiguous)
+ *   bias  [N]     dtype or NULL
+ *   y     [M, N]  dtype, row stride ldy
+ * dtype is SELAS_BF16 (fp32 accumulation, one rounding of acc + bias).
+ * M <= 32 runs a skinny dequant-GEMM, larger M a tiled MFMA GEMM with the
+ * dequantization fused into the operand load. Returns SELAS_EUNSUPPORTED
+ * when the shape or layout is outside the fused kernels (blocksize != 64,
+ * K % 64 != 0, misaligned rows, dtype other than bf16); the caller then
+ * decodes with selas_nf4_dequant and uses a library GEMM.
+ * Replaces UnitView.linear for NF4 weights (selas/store.py:289-293):
+ * decode (codecs.py:269-280) followed by F.linear.
+ */
+int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uint8_t *packed,
+                     const float *absmax, int64_t blocksize, const float code[16], int64_t N,
+                     const void *bias, void *y, int64_t ldy, int dtype, void *stream);
+
+/* ------------------------------------------------------------ segments
+ *
+ * The memory-bound code between the block linears (selas/models/flux.py:
+ * 164-200). Tensors are [B, L, D] with D contiguous; `sb`/`sl` are the batch
+ * and row strides in elements. Per-batch vectors (shift, scale, gate) are
+ * [B, D] with batch stride `mod_sb`. Outputs are contiguous. All math is fp32.
+ */
+
+/* out = dtype(LayerNorm(x; no affine, eps 1e-6) * (1 + scale) + shift).
+ * Replaces _mod_in (flux.py:164-166) with _ln (flux.py:146-147). */
+int selas_mod_in(const float *x, int64_t B, int64_t L, int64_t D, int64_t x_sb, int64_t x_sl,
+                 const float *shift, const float *scale, int64_t mod_sb, void *out, int out_dtype,
+                 void *stream);
+
+/* out = x + g * float(y), y clamped to +-65504 first when guard != 0.
+ * Replaces _gated_add (flux.py:169-171) with _res (flux.py:141-143). */
+int selas_gated_add(const float *x, int64_t B, int64_t L, int64_t D, int64_t x_sb, int64_t x_sl,
+                    const float *g, int64_t g_sb, const void *y, int y_dtype, int64_t y_sb, int64_t y_sl,
+                    int guard, float *out, void *stream);
+
+/* x_out = x + g * float(y) as above, and h = mod_in(x_out, shift, scale) in one pass.
+ * Replaces _gated_add_mod (flux.py:174-176). */
+int selas_gated_add_mod(const float *x, int64_t B, int64_t L, int64_t D, int64_t x_sb, int64_t x_sl,
+                        const float *g, int64_t g_sb, const void *y, int y_dtype, int64_t y_sb, int64_t y_sl,
+                        int guard, const float *shift, const float *scale, int64_t mod_sb, float *x_out,
+                        void *h, int h_dtype, void *stream);
+
+/* Single-stream attention prep: qkv [B, L, 3*H*Dh] (channel = which*H*Dh + h*Dh + d,
+ * strides qkv_sb, qkv_sl) -> q, k = dtype(RoPE(RMSNorm(.) * scale)), v = copy,
+ * each [B, H, L, Dh] contiguous. RMSNorm eps 1e-6 over Dh in fp32; RoPE rotates
+ * interleaved pairs with cos/sin [L, Dh/2] fp32. Dh must be 128.
+ * Replaces _qkv_single (flux.py:188-191) with _heads, qk_rms, apply_rope (117-132). */
+int selas_qkv_single(const void *qkv, int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t qkv_sb,
+                     int64_t qkv_sl, const float *q_scale, const float *k_scale, const float *cos,
+                     const float *sin, void *q, void *k, void *v, int dtype, void *stream);
+
+/* Double-stream attention prep: text qkv [B, Lt, 3HDh] and image qkv [B, Li, 3HDh],
+ * each normalised with its own q/k scales, joined text-first along L, RoPE with
+ * cos/sin [Lt+Li, Dh/2]; q, k, v [B, H, Lt+Li, Dh] contiguous.
+ * Replaces _qkv_double (flux.py:179-185). */
+int selas_qkv_double(const void *tqkv, int64_t t_sb, int64_t t_sl, int64_t Lt, const void *iqkv, int64_t i_sb,
+                     int64_t i_sl, int64_t Li, int64_t B, int64_t H, int64_t Dh, const float *tq_scale,
+                     const float *tk_scale, const float *iq_scale, const float *ik_scale, const float *cos,
+                     const float *sin, void *q, void *k, void *v, int dtype, void *stream);
+
+/* out = gelu_tanh(h) for rows x cols (row stride ld), out contiguous.
+ * Replaces _gelu (flux.py:194-195). */
+int selas_gelu(const void *h, int64_t rows, int64_t cols, int64_t ld, void *out, int dtype, void *stream);
+
+/* out[r] = concat(attn[r] (Da), gelu_tanh(mlp[r]) (Dm)), out [rows, Da+Dm] contiguous.
+ * Replaces _attn_mlp (flux.py:198-200). */
+int selas_attn_mlp(const void *attn, int64_t rows, int64_t Da, int64_t lda, const void *mlp, int64_t Dm,
+                   int64_t ldm, void *out, int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SELAS_AMD_H */

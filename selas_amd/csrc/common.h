@@ -1,0 +1,90 @@
+// Shared helpers for the gfx950 kernels and their C-ABI wrappers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/selas_amd.h"
+
+namespace selas {
+
+// ------------------------------------------------------------------ host side
+
+// Records a formatted message for selas_last_error() and returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the message and returns SELAS_OK.
+int ok();
+// Turns the launch status of the last kernel into a return code.
+int check_launch(const char *what);
+
+inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool valid_dtype(int dt) { return dt == SELAS_F32 || dt == SELAS_F16 || dt == SELAS_BF16; }
+inline const char *dtype_name(int dt) {
+  return dt == SELAS_F32 ? "f32" : dt == SELAS_F16 ? "f16" : dt == SELAS_BF16 ? "bf16" : "?";
+}
+
+// The 16-entry codebook, passed by value so that it lives in scalar registers.
+struct Code16 {
+  float v[16];
+};
+
+// ------------------------------------------------------------------ device side
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// fp32 -> bf16 bits, round to nearest even (the rounding torch uses for
+// bfloat16 casts). Any NaN becomes the quiet NaN 0x7FC0.
+__device__ __forceinline__ uint16_t bf16_bits_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// fp32 -> fp16 bits, IEEE round to nearest even (overflow to inf, gradual
+// underflow), done by the hardware convert.
+__device__ __forceinline__ uint16_t f16_bits_rne(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+// Loads element i of a 16-bit or 32-bit float array as fp32.
+template <int DT>
+__device__ __forceinline__ float load_f(const void *p, int64_t i) {
+  if constexpr (DT == SELAS_F32) return static_cast<const float *>(p)[i];
+  else if constexpr (DT == SELAS_F16) return f16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  else return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+}
+
+// Rounds fp32 to the storage type DT and stores element i.
+template <int DT>
+__device__ __forceinline__ void store_f(void *p, int64_t i, float v) {
+  if constexpr (DT == SELAS_F32) static_cast<float *>(p)[i] = v;
+  else if constexpr (DT == SELAS_F16) static_cast<uint16_t *>(p)[i] = f16_bits_rne(v);
+  else static_cast<uint16_t *>(p)[i] = bf16_bits_rne(v);
+}
+
+// Two fp32 values -> packed (lo, hi) bf16 pair with the gfx950 hardware convert
+// (round to nearest even; identical to bf16_bits_rne for every non-NaN value).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Wave-wide (64 lanes) reductions through the cross-lane network.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace selas

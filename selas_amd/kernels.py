@@ -1,0 +1,208 @@
+"""The elementwise segments of a FLUX block as gfx950 kernels, with the reference's interface.
+
+``Kernels`` has the seven segment methods of selas.models.flux.Kernels
+(flux.py:206-212) with the same names, arguments and return values, so an
+instance can be passed as ``kernels=`` to selas's FluxRunner or ``k=`` to its
+block functions. Each method is one kernel launch on the current stream; the
+fp32 math matches the eager segments (flux.py:164-200) up to rounding.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+SEGMENT_NAMES = ("mod_in", "gated_add", "gated_add_mod", "qkv_double", "qkv_single", "gelu", "attn_mlp")
+
+
+def _bld(x: torch.Tensor, what: str) -> tuple[int, int, int, int, int]:
+    """(B, L, D, batch stride, row stride) of a [B, L, D] or [L, D] tensor with unit column stride."""
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    if x.dim() != 3 or x.stride(-1) != 1:
+        raise ValueError(f"{what}: expected [B, L, D] with contiguous D, got shape {tuple(x.shape)} "
+                         f"strides {x.stride()}")
+    b, l, d = x.shape
+    return b, l, d, x.stride(0) if b > 1 else 0, x.stride(1) if l > 1 else d
+
+
+def _vec(v: torch.Tensor, b: int, d: int, what: str) -> tuple[torch.Tensor, int]:
+    """A per-batch modulation vector ([B|1, 1, D], [B|1, D] or [D]) as fp32 plus its batch stride."""
+    if v.dtype != torch.float32:
+        v = v.float()
+    if v.shape[-1] != d or v.stride(-1) != 1:
+        v = v.contiguous()
+    if v.dim() == 3:
+        if v.shape[1] != 1:
+            raise ValueError(f"{what}: expected [B, 1, D], got {tuple(v.shape)}")
+        vb, sb = v.shape[0], v.stride(0)
+    elif v.dim() == 2:
+        vb, sb = v.shape[0], v.stride(0)
+    elif v.dim() == 1:
+        vb, sb = 1, 0
+    else:
+        raise ValueError(f"{what}: bad vector shape {tuple(v.shape)}")
+    if v.shape[-1] != d or vb not in (1, b):
+        raise ValueError(f"{what}: vector {tuple(v.shape)} does not broadcast over batch {b}, width {d}")
+    return v, (sb if vb > 1 else 0)
+
+
+def _f32_rows(x: torch.Tensor, what: str) -> torch.Tensor:
+    if x.dtype != torch.float32:
+        raise ValueError(f"{what}: the residual stream must be float32, got {x.dtype}")
+    return x
+
+
+class Kernels:
+    """The segments of a block (mod_in, gated_add, gated_add_mod, qkv_double, qkv_single, gelu, attn_mlp)."""
+
+    compiled = True  # fused kernels (the reference's Kernels(compiled=True) role)
+
+    # ------------------------------------------------------------------ LayerNorm + adaLN
+    def mod_in(self, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+        """``(LN(x) * (1 + scale) + shift).to(dt)`` (flux.py:164-166)."""
+        x = _f32_rows(x, "mod_in")
+        dev = _lib.require_gpu(x, shift, scale)
+        b, l, d, sb, sl = _bld(x, "mod_in")
+        shift, msb = _vec(shift, b, d, "mod_in shift")
+        scale, csb = _vec(scale, b, d, "mod_in scale")
+        if msb != csb:
+            raise ValueError("mod_in: shift and scale must share a batch stride")
+        out = torch.empty(*x.shape, dtype=dt, device=dev)
+        with torch.cuda.device(dev):
+            _lib.call("selas_mod_in", x.data_ptr(), b, l, d, sb, sl, shift.data_ptr(), scale.data_ptr(), msb,
+                      out.data_ptr(), _lib.dtype_code(dt), _lib.stream(dev))
+        return out
+
+    # ------------------------------------------------------------------ gated residual
+    def gated_add(self, x: torch.Tensor, g: torch.Tensor, y: torch.Tensor, guard: bool) -> torch.Tensor:
+        """``x + g * float(y)`` with y clamped to the fp16 range when ``guard`` (flux.py:169-171)."""
+        return self._gated(x, g, y, guard, None, None, None)[0]
+
+    def gated_add_mod(self, x, g, y, shift, scale, dt, guard: bool):
+        """``(x', mod_in(x', shift, scale, dt))`` with ``x' = gated_add(x, g, y, guard)`` (flux.py:174-176)."""
+        return self._gated(x, g, y, guard, shift, scale, dt)
+
+    def _gated(self, x, g, y, guard, shift, scale, dt):
+        what = "gated_add" if shift is None else "gated_add_mod"
+        x = _f32_rows(x, what)
+        dev = _lib.require_gpu(x, g, y, shift, scale)
+        b, l, d, sb, sl = _bld(x, what)
+        yb, yl, yd, ysb, ysl = _bld(y, what + " y")
+        if (yb, yl, yd) != (b, l, d):
+            raise ValueError(f"{what}: y {tuple(y.shape)} does not match x {tuple(x.shape)}")
+        g, gsb = _vec(g, b, d, what + " gate")
+        x_out = torch.empty(*x.shape, dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            if shift is None:
+                _lib.call("selas_gated_add", x.data_ptr(), b, l, d, sb, sl, g.data_ptr(), gsb, y.data_ptr(),
+                          _lib.dtype_code(y.dtype), ysb, ysl, int(bool(guard)), x_out.data_ptr(), _lib.stream(dev))
+                return x_out, None
+            shift, msb = _vec(shift, b, d, what + " shift")
+            scale, csb = _vec(scale, b, d, what + " scale")
+            if msb != csb:
+                raise ValueError(f"{what}: shift and scale must share a batch stride")
+            h = torch.empty(*x.shape, dtype=dt, device=dev)
+            _lib.call("selas_gated_add_mod", x.data_ptr(), b, l, d, sb, sl, g.data_ptr(), gsb, y.data_ptr(),
+                      _lib.dtype_code(y.dtype), ysb, ysl, int(bool(guard)), shift.data_ptr(), scale.data_ptr(), msb,
+                      x_out.data_ptr(), h.data_ptr(), _lib.dtype_code(dt), _lib.stream(dev))
+        return x_out, h
+
+    # ------------------------------------------------------------------ attention prep
+    @staticmethod
+    def _heads_src(qkv: torch.Tensor, heads: int, what: str):
+        if qkv.dim() != 3 or qkv.stride(-1) != 1:
+            raise ValueError(f"{what}: qkv must be [B, L, 3*H*Dh] with contiguous channels")
+        b, l, c = qkv.shape
+        if c % (3 * heads):
+            raise ValueError(f"{what}: {c} channels do not split into 3 x {heads} heads")
+        return b, l, c // (3 * heads), qkv.stride(0) if b > 1 else 0, qkv.stride(1) if l > 1 else c
+
+    @staticmethod
+    def _scale(s: torch.Tensor, dh: int) -> torch.Tensor:
+        s = s.reshape(-1)
+        if s.numel() != dh:
+            raise ValueError(f"norm scale has {s.numel()} values, head_dim is {dh}")
+        return s.float().contiguous()
+
+    def qkv_single(self, qkv, qs, ks, cos, sin, heads: int, dt):
+        """(q, k, v) [B, H, L, Dh] from linear1's qkv view (flux.py:188-191)."""
+        dev = _lib.require_gpu(qkv, qs, ks, cos, sin)
+        b, l, dh, sb, sl = self._heads_src(qkv, heads, "qkv_single")
+        if qkv.dtype != dt:
+            raise ValueError(f"qkv_single: qkv is {qkv.dtype}, compute dtype is {dt}")
+        cos, sin = cos.float().contiguous(), sin.float().contiguous()
+        if cos.shape != (l, dh // 2) or sin.shape != (l, dh // 2):
+            raise ValueError(f"qkv_single: rope tables {tuple(cos.shape)} do not match L={l}, head_dim={dh}")
+        qs, ks = self._scale(qs, dh), self._scale(ks, dh)
+        q, k, v = (torch.empty(b, heads, l, dh, dtype=dt, device=dev) for _ in range(3))
+        with torch.cuda.device(dev):
+            _lib.call("selas_qkv_single", qkv.data_ptr(), b, l, heads, dh, sb, sl, qs.data_ptr(), ks.data_ptr(),
+                      cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.dtype_code(dt),
+                      _lib.stream(dev))
+        return q, k, v
+
+    def qkv_double(self, tqkv, iqkv, tqs, tks, iqs, iks, cos, sin, heads: int, dt):
+        """(q, k, v) [B, H, Lt+Li, Dh], text first, per-stream QK norms (flux.py:179-185)."""
+        dev = _lib.require_gpu(tqkv, iqkv, tqs, tks, iqs, iks, cos, sin)
+        tb, lt, dh, tsb, tsl = self._heads_src(tqkv, heads, "qkv_double txt")
+        ib, li, dhi, isb, isl = self._heads_src(iqkv, heads, "qkv_double img")
+        if tb != ib or dh != dhi:
+            raise ValueError(f"qkv_double: txt {tuple(tqkv.shape)} and img {tuple(iqkv.shape)} disagree")
+        if tqkv.dtype != dt or iqkv.dtype != dt:
+            raise ValueError(f"qkv_double: qkv dtypes {tqkv.dtype}/{iqkv.dtype}, compute dtype is {dt}")
+        cos, sin = cos.float().contiguous(), sin.float().contiguous()
+        if cos.shape != (lt + li, dh // 2) or sin.shape != (lt + li, dh // 2):
+            raise ValueError(f"qkv_double: rope tables {tuple(cos.shape)} do not match L={lt + li}, head_dim={dh}")
+        tqs, tks, iqs, iks = (self._scale(s, dh) for s in (tqs, tks, iqs, iks))
+        q, k, v = (torch.empty(tb, heads, lt + li, dh, dtype=dt, device=dev) for _ in range(3))
+        with torch.cuda.device(dev):
+            _lib.call("selas_qkv_double", tqkv.data_ptr(), tsb, tsl, lt, iqkv.data_ptr(), isb, isl, li, tb, heads,
+                      dh, tqs.data_ptr(), tks.data_ptr(), iqs.data_ptr(), iks.data_ptr(), cos.data_ptr(),
+                      sin.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.dtype_code(dt), _lib.stream(dev))
+        return q, k, v
+
+    # ------------------------------------------------------------------ MLP activation
+    @staticmethod
+    def _rows2(t: torch.Tensor, what: str) -> tuple[int, int, int]:
+        """(rows, cols, row stride) of a tensor whose leading dims collapse onto one row stride."""
+        if t.stride(-1) != 1:
+            raise ValueError(f"{what}: last dim must be contiguous")
+        cols = t.shape[-1]
+        rows = t.numel() // cols if cols else 0
+        if t.dim() == 1:
+            return 1, cols, cols
+        ld = t.stride(-2) if t.shape[-2] > 1 else cols
+        expect = ld
+        for i in range(t.dim() - 2, 0, -1):  # outer dims must be dense over rows of stride ld
+            expect *= t.shape[i]
+            if t.shape[i - 1] > 1 and t.stride(i - 1) != expect:
+                raise ValueError(f"{what}: rows do not share one stride")
+        return rows, cols, ld
+
+    def gelu(self, h: torch.Tensor) -> torch.Tensor:
+        """GELU with the tanh approximation (flux.py:194-195)."""
+        dev = _lib.require_gpu(h)
+        rows, cols, ld = self._rows2(h, "gelu")
+        out = torch.empty(*h.shape, dtype=h.dtype, device=dev)
+        with torch.cuda.device(dev):
+            _lib.call("selas_gelu", h.data_ptr(), rows, cols, ld, out.data_ptr(), _lib.dtype_code(h.dtype),
+                      _lib.stream(dev))
+        return out
+
+    def attn_mlp(self, attn: torch.Tensor, mlp: torch.Tensor) -> torch.Tensor:
+        """``cat((attn, gelu(mlp)), dim=2)``: linear2's input (flux.py:198-200)."""
+        dev = _lib.require_gpu(attn, mlp)
+        if attn.shape[:-1] != mlp.shape[:-1] or attn.dtype != mlp.dtype:
+            raise ValueError(f"attn_mlp: attn {tuple(attn.shape)} {attn.dtype} vs mlp {tuple(mlp.shape)} {mlp.dtype}")
+        ra, da, lda = self._rows2(attn, "attn_mlp attn")
+        rm, dm, ldm = self._rows2(mlp, "attn_mlp mlp")
+        out = torch.empty(*attn.shape[:-1], da + dm, dtype=attn.dtype, device=dev)
+        with torch.cuda.device(dev):
+            _lib.call("selas_attn_mlp", attn.data_ptr(), ra, da, lda, mlp.data_ptr(), dm, ldm, out.data_ptr(),
+                      _lib.dtype_code(attn.dtype), _lib.stream(dev))
+        return out
+
+
+FUSED = Kernels()

@@ -1,0 +1,102 @@
+"""FLUX blocks on the GPU (fused NF4 linears + segment kernels + SDPA) against the oracle blocks on
+the CPU in fp32 with the same decoded NF4 operands (oracle/flux.py, pinned by reference goldens).
+
+Tolerance: the GPU path rounds activations to bf16 between kernels, so block outputs are compared
+on the residual update (out - in): relative L2 <= 2e-2, and the fp32 stream itself <= 4e-3.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import flux as OF
+from oracle import segments as S
+from selas_amd import flux as F
+
+from .conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+CFG = F.FluxConfig(hidden=256, heads=2, mlp_hidden=1024, depth_double=2, depth_single=2, in_channels=64,
+                   context_dim=128, vec_dim=64, axes_dim=(16, 56, 56))
+OCFG = OF.FluxConfig(hidden=256, heads=2, mlp_hidden=1024, depth_double=2, depth_single=2, in_channels=64,
+                     context_dim=128, vec_dim=64, axes_dim=(16, 56, 56))
+
+
+def oracle_unit(view):
+    enc = {n: (e.codec, e.shape, e.meta, {k: v.cpu() for k, v in e.parts.items()}) for n, e in view.tensors.items()}
+    return OF.OracleUnit.from_encoded(enc, torch.float32)
+
+
+def rel(a, b):
+    return ((a.double().cpu() - b.double()).norm() / b.double().norm()).item()
+
+
+@pytest.fixture(scope="module")
+def model():
+    return F.RandomFlux(CFG, "cuda", torch.bfloat16, seed=3)
+
+
+def inputs(b, lt, grid):
+    g = seeded(21)
+    li = grid * grid
+    img = torch.randn(b, li, CFG.hidden, generator=g)
+    txt = torch.randn(b, lt, CFG.hidden, generator=g)
+    ids = torch.cat((torch.zeros(lt, 3), F.image_ids(grid, grid)), dim=0)
+    cos, sin = S.rope_tables(ids, CFG.axes_dim, CFG.theta)
+    return img, txt, cos, sin
+
+
+def test_double_block(model):
+    img, txt, cos, sin = inputs(2, 64, 8)
+    mod = (torch.randn(2, 12 * CFG.hidden, generator=seeded(22)) * 0.3).to(torch.bfloat16)
+    dev = torch.device("cuda")
+    gi, gt = F.double_block(model.doubles[0], img.to(dev), txt.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG,
+                            torch.bfloat16, False)
+    ri, rt = OF.double_block(oracle_unit(model.doubles[0]), img, txt, mod.float(), cos, sin, OCFG, torch.float32, False)
+    assert rel(gi - img.cuda(), ri - img) < 2e-2 and rel(gt - txt.cuda(), rt - txt) < 2e-2
+    assert rel(gi, ri) < 4e-3 and rel(gt, rt) < 4e-3
+
+
+def test_single_block(model):
+    img, txt, cos, sin = inputs(1, 64, 8)
+    x = torch.cat((txt, img), dim=1)
+    mod = (torch.randn(1, 3 * CFG.hidden, generator=seeded(23)) * 0.3).to(torch.bfloat16)
+    dev = torch.device("cuda")
+    gx = F.single_block(model.singles[0], x.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
+                        False)
+    rx = OF.single_block(oracle_unit(model.singles[0]), x, mod.float(), cos, sin, OCFG, torch.float32, False)
+    assert rel(gx - x.cuda(), rx - x) < 2e-2 and rel(gx, rx) < 4e-3
+
+
+def test_modulations_and_step(model):
+    # hoisted modulation GEMVs (M = steps = 5) and one step through 2 double + 2 single blocks
+    dev = torch.device("cuda")
+    sv = torch.nn.functional.silu(torch.randn(5, 1, CFG.hidden, generator=seeded(24))).to(torch.bfloat16)
+    mods = model.modulations(sv.to(dev))
+    units = [oracle_unit(u) for u in model.mods]
+    for i, (m, u) in enumerate(zip(mods, units)):
+        if i < len(model.doubles):
+            ref = torch.cat((u.linear(sv.float(), "img_mod.lin"), u.linear(sv.float(), "txt_mod.lin")), dim=-1)
+        else:
+            ref = u.linear(sv.float(), "modulation.lin")
+        assert m.shape == ref.shape and rel(m, ref) < 4e-3
+    img, txt, cos, sin = inputs(1, 64, 8)
+    lat = torch.randn(1, 64, 64, generator=seeded(25))
+    fmod = (torch.randn(1, 2 * CFG.hidden, generator=seeded(26)) * 0.3).to(torch.bfloat16)
+    s = 2
+    out = model.step(lat.to(dev), txt.to(dev), [m[s] for m in mods], fmod.to(dev), cos.to(dev), sin.to(dev))
+    g = oracle_unit(model.globals)
+    x_img = g.linear(lat.to(torch.bfloat16).float(), "img_in")
+    t = txt
+    for i, w in enumerate(model.doubles):
+        x_img, t = OF.double_block(oracle_unit(w), x_img, t, mods[i][s].float().cpu(), cos, sin, OCFG, torch.float32,
+                                   False)
+    x = torch.cat((t, x_img), dim=1)
+    for j, w in enumerate(model.singles):
+        x = OF.single_block(oracle_unit(w), x, mods[len(model.doubles) + j][s].float().cpu(), cos, sin, OCFG,
+                            torch.float32, False)
+    ref = OF.final_layer(g, x[:, 64:], fmod.float(), torch.float32)
+    assert out.shape == (1, 64, 64) and torch.isfinite(out).all()
+    assert rel(out, ref) < 3e-2

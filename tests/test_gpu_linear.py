@@ -1,0 +1,143 @@
+"""Quantized linear on the GPU (fused-dequant MFMA GEMM for M > 32, skinny dequant-GEMM for
+M <= 32) against the oracle: x @ decode(W).T + b with fp32 accumulation in fp64 on the CPU.
+
+Tolerance (stated by the path's contract): max |y - ref| <= 1e-2 * max |ref| and relative
+L2 error <= 4e-3. The fused GEMM's weight operand is additionally checked bit-exact with
+one-hot inputs (x = e_k gives y[:, n] = W_bf16[n, k] exactly).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4 as onf4
+from selas_amd import codecs
+from selas_amd.linear import UnitView, nf4_linear
+
+from .conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL, L2_REL = 1e-2, 4e-3
+
+
+def make_weight(n, k, seed, dev, bs=64, scale=0.02):
+    w = torch.randn(n, k, generator=seeded(seed)) * scale
+    p, a = onf4.encode(w.numpy(), bs)
+    ref = torch.from_numpy(onf4.bf16_to_f32(onf4.decode(p, a, bs, out=onf4.BF16))).view(n, k)
+    return torch.from_numpy(p).to(dev), torch.from_numpy(a).to(dev), ref
+
+
+def oracle_linear(x, w_ref, bias=None):
+    y = x.double().cpu() @ w_ref.double().t()
+    if bias is not None:
+        y = y + bias.double().cpu()
+    return y
+
+
+def check_close(y, ref):
+    y = y.double().cpu()
+    err = (y - ref).abs().max().item()
+    assert err <= MAX_REL * ref.abs().max().item(), f"max abs err {err} vs max {ref.abs().max().item()}"
+    rel = ((y - ref).norm() / ref.norm()).item()
+    assert rel <= L2_REL, f"relative L2 {rel}"
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 100, 128), (28, 9216, 3072), (32, 192, 3072), (3, 4160, 640)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_skinny_path(dev, m, n, k, with_bias):
+    p, a, w_ref = make_weight(n, k, m + n, dev)
+    x = (torch.randn(m, k, generator=seeded(1)).to(torch.bfloat16)).to(dev)
+    b = (torch.randn(n, generator=seeded(2)) * 0.02).to(torch.bfloat16).to(dev) if with_bias else None
+    y = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    check_close(y, oracle_linear(x, w_ref, b))
+
+
+@pytest.mark.parametrize("m,n,k", [(33, 64, 64), (100, 96, 128), (256, 256, 3072), (257, 300, 192),
+                                   (513, 3072, 640), (1536, 512, 3072)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_tiled_path(dev, m, n, k, with_bias):
+    p, a, w_ref = make_weight(n, k, m + n + k, dev)
+    x = torch.randn(m, k, generator=seeded(3)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(4)) * 0.02).to(torch.bfloat16).to(dev) if with_bias else None
+    y = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    check_close(y, oracle_linear(x, w_ref, b))
+
+
+def test_tiled_operand_is_the_reference_decode_bit_for_bit(dev):
+    n, k, m = 320, 640, 96
+    p, a, w_ref = make_weight(n, k, 7, dev)
+    ks = torch.randint(0, k, (m,), generator=seeded(8))
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    x[torch.arange(m), ks] = 1.0
+    y = nf4_linear(x.to(dev), p, a, 64, codecs.NF4_CODE, (n, k)).float().cpu()
+    assert torch.equal(y, w_ref[:, ks].t())
+
+
+def test_skinny_operand_within_one_rounding(dev):
+    n, k, m = 192, 256, 16
+    p, a, w_ref = make_weight(n, k, 9, dev)
+    ks = torch.randint(0, k, (m,), generator=seeded(10))
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    x[torch.arange(m), ks] = 1.0
+    y = nf4_linear(x.to(dev), p, a, 64, codecs.NF4_CODE, (n, k)).float().cpu()
+    ref = w_ref[:, ks].t()
+    assert ((y - ref).abs() <= 2.0 ** -7 * ref.abs()).all()
+
+
+def test_strided_and_batched_inputs(dev):
+    n, k = 256, 192
+    p, a, w_ref = make_weight(n, k, 11, dev)
+    base = torch.randn(2, 70, k + 64, generator=seeded(12)).to(torch.bfloat16).to(dev)
+    x = base[:, 3:, 32:32 + k]  # [2, 67, k] with row stride k+64, batch stride 70*(k+64)
+    y = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k))
+    assert y.shape == (2, 67, n)
+    check_close(y.reshape(-1, n), oracle_linear(x.reshape(-1, k), w_ref))
+
+
+def test_unsupported_shapes_fall_back_to_decode_and_library_gemm(dev):
+    n, k = 96, 96  # K % 64 != 0 with blocksize 32
+    p, a, w_ref = make_weight(n, k, 13, dev, bs=32)
+    x = torch.randn(40, k, generator=seeded(14)).to(torch.bfloat16).to(dev)
+    y = nf4_linear(x, p, a, 32, codecs.NF4_CODE, (n, k))
+    check_close(y, oracle_linear(x, w_ref))
+
+
+def test_deterministic_across_calls(dev):
+    n, k = 3072, 3072
+    p, a, _ = make_weight(n, k, 15, dev)
+    for m in (28, 300):
+        x = torch.randn(m, k, generator=seeded(16)).to(torch.bfloat16).to(dev)
+        y1 = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k))
+        y2 = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k))
+        assert torch.equal(y1, y2)
+
+
+def test_unit_view_linear(dev):
+    n, k = 128, 256
+    w = torch.randn(n, k, generator=seeded(17)) * 0.02
+    e = codecs.encode_nf4("lin.weight", w.to(dev))
+    b = codecs.encode_raw("lin.bias", (torch.randn(n, generator=seeded(18)) * 0.02).to(dev), torch.bfloat16)
+    view = UnitView({"lin.weight": e, "lin.bias": b}, torch.bfloat16)
+    x = torch.randn(1, 80, k, generator=seeded(19)).to(torch.bfloat16).to(dev)
+    y = view.linear(x, "lin")
+    w_ref = view.get("lin.weight").float().cpu()
+    check_close(y.reshape(-1, n), oracle_linear(x.reshape(-1, k), w_ref, b.parts["data"]))
+    assert view.get("lin.bias").data_ptr() == b.parts["data"].data_ptr()
+
+
+def test_full_size_single_linear(dev):
+    # config 1: W 12288x3072 ~ N(0, 0.02) seed 0, X 1536x3072 bf16 ~ N(0, 1) seed 1; rows sampled for the oracle
+    n, k, m = 12288, 3072, 1536
+    w = torch.randn(n, k, generator=seeded(0)) * 0.02
+    e = codecs.encode_nf4("w", w.to(dev))
+    x = torch.randn(m, k, generator=seeded(1)).to(torch.bfloat16).to(dev)
+    y = nf4_linear(x, e.parts["packed"], e.parts["absmax"], 64, codecs.NF4_CODE, (n, k))
+    dec = onf4.decode(e.parts["packed"].cpu().numpy(), e.parts["absmax"].cpu().numpy(), 64, out=onf4.BF16)
+    w_ref = torch.from_numpy(onf4.bf16_to_f32(dec)).view(n, k)
+    rows = torch.randint(0, m, (64,), generator=seeded(2))
+    check_close(y[rows], oracle_linear(x[rows], w_ref))
+    assert torch.isfinite(y).all()

@@ -44,10 +44,19 @@ __device__ __forceinline__ uint16_t bf16_bits_rne(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Returns `v` unchanged but opaque to the optimiser (no instruction is
+// emitted): a conversion of the result can then not be merged with the
+// arithmetic that produced `v` (for example fp16(a * b) into one
+// mixed-precision FMA that rounds the exact product once).
+__device__ __forceinline__ float materialize(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // fp32 -> fp16 bits, IEEE round to nearest even (overflow to inf, gradual
-// underflow), done by the hardware convert.
+// underflow), done by the hardware convert on the already-rounded fp32 value.
 __device__ __forceinline__ uint16_t f16_bits_rne(float f) {
-  _Float16 h = static_cast<_Float16>(f);
+  _Float16 h = static_cast<_Float16>(materialize(f));
   return __builtin_bit_cast(uint16_t, h);
 }
 
@@ -76,7 +85,7 @@ __device__ __forceinline__ void store_f(void *p, int64_t i, float v) {
 // (round to nearest even; identical to bf16_bits_rne for every non-NaN value).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  bf16x2 v = {static_cast<__bf16>(materialize(lo)), static_cast<__bf16>(materialize(hi))};
   return __builtin_bit_cast(uint32_t, v);
 }
 

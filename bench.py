@@ -186,16 +186,22 @@ def bench_library_path(dev, steps, warmup):
 
 
 def bench_modulations(dev, steps, warmup):
-    """76 hoisted adaLN linears at M = 28 (19 double blocks x img/txt 3072 -> 18432, 38 single 3072 -> 9216)."""
+    """76 hoisted adaLN linears at M = 28 (19 double blocks x img/txt 3072 -> 18432, 38 single 3072 -> 9216),
+    76 distinct weights (1.8 GB of NF4, beyond the 256 MB Infinity Cache): one grouped launch, and one launch
+    per linear."""
+    from selas_amd import codecs
+    from selas_amd.linear import nf4_linear_grouped
+
     s = 28
     ws = [nf4_weight(6 * D, D, 400 + i, dev) for i in range(38)] + [nf4_weight(3 * D, D, 500 + i, dev) for i in range(38)]
     bs = [bias(e.shape[0], 600 + i, dev) for i, e in enumerate(ws)]
     g = torch.Generator(device=dev).manual_seed(7)
     x = torch.nn.functional.silu(torch.randn(s, D, generator=g, device=dev)).to(torch.bfloat16)
-    nbytes = sum(e.nbytes for e in ws) + sum(b.numel() * 2 for b in bs) + 76 * s * D * 2 + sum(s * e.shape[0] * 2 for e in ws)
+    nbytes = sum(e.nbytes for e in ws) + sum(b.numel() * 2 for b in bs) + s * D * 2 + sum(s * e.shape[0] * 2 for e in ws)
     flops = sum(2.0 * s * e.shape[0] * D for e in ws)
+    tuples = [(e.parts["packed"], e.parts["absmax"], 64, codecs.NF4_CODE, e.shape, b) for e, b in zip(ws, bs)]
 
-    def run(tm=None):
+    def run_each(tm=None):
         for e, b in zip(ws, bs):
             t = tm.start("gemv") if tm else None
             lin(x, e, b)
@@ -203,20 +209,21 @@ def bench_modulations(dev, steps, warmup):
                 tm.stop(t)
 
     for _ in range(warmup):
-        run()
+        run_each()
+        nf4_linear_grouped(x, tuples)
     torch.cuda.synchronize(dev)
-    reps = max(1, steps // 4)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        run()
-    torch.cuda.synchronize(dev)
-    wall = (time.perf_counter() - t0) / reps
     tm = Timer()
-    run(tm)
+    run_each(tm)
+    for _ in range(max(3, steps // 2)):
+        t = tm.start("grouped")
+        nf4_linear_grouped(x, tuples)
+        tm.stop(t)
     torch.cuda.synchronize(dev)
     per = tm.mean_ms("gemv")
-    return {"launches": 76, "bytes": nbytes, "flops": flops, "wall_ms": wall * 1e3, "gbs_wall": nbytes / wall / 1e9,
-            "kernel_ms_mean": per, "gbs_kernel": nbytes / (per * 76) / 1e6}
+    grp = tm.mean_ms("grouped")
+    return {"launches": 76, "bytes": nbytes, "flops": flops, "grouped_ms": grp, "gbs_grouped": nbytes / grp / 1e6,
+            "frac_hbm_grouped": nbytes / grp / 1e6 / PEAK_HBM_GBS, "per_linear_kernel_ms_mean": per,
+            "gbs_per_linear": nbytes / (per * 76) / 1e6}
 
 
 def bench_segments(dev, steps, warmup):
@@ -366,7 +373,8 @@ def main():
         extra["single_linear_1536"] = bench_single_linear(dev, a.steps, a.warmup)
         log(f"bench: single linear {extra['single_linear_1536']['tflops']:.1f} TFLOP/s")
         extra["modulations_m28"] = bench_modulations(dev, a.steps, a.warmup)
-        log(f"bench: modulations {extra['modulations_m28']['gbs_kernel']:.0f} GB/s")
+        mo = extra['modulations_m28']
+        log(f"bench: modulations grouped {mo['gbs_grouped']:.0f} GB/s, per-linear {mo['gbs_per_linear']:.0f} GB/s")
         extra["segments_m4608"] = bench_segments(dev, a.steps, a.warmup)
         log(f"bench: segments {json.dumps({k: round(v['gbs']) for k, v in extra['segments_m4608'].items()})}")
         extra["library_path"] = bench_library_path(dev, a.steps, a.warmup)

@@ -91,6 +91,34 @@ int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uin
                      const float *absmax, int64_t blocksize, const float code[16], int64_t N,
                      const void *bias, void *y, int64_t ldy, int dtype, void *stream);
 
+/*
+ * One NF4 weight of a grouped skinny linear (device-memory array element).
+ * packed/absmax as for selas_nf4_linear, bias [n] bf16 or NULL, y [M, n] bf16
+ * with row stride ldy. The layout is fixed: 4 pointers then 2 int64.
+ */
+typedef struct selas_nf4_gemv_desc {
+  const uint8_t *packed;
+  const float *absmax;
+  const void *bias;
+  void *y;
+  int64_t n;
+  int64_t ldy;
+} selas_nf4_gemv_desc;
+
+/*
+ * `count` quantized linears that share one input x [M, K] (M <= 32, K <= 3072,
+ * K % 64 == 0, blocksize 64, bf16), computed by one launch: y_i = x W_i^T + b_i.
+ * `descs` is a device array of `count` descriptors and total_n the sum of
+ * their n (it sizes the launch). Each output has the bits selas_nf4_linear
+ * gives for that weight alone.
+ * Replaces the per-unit loop of FluxRunner.modulations (selas/models/flux.py:
+ * 428-445), which calls UnitView.linear once per modulation weight with the
+ * same silu(vec) input.
+ */
+int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx, const selas_nf4_gemv_desc *descs,
+                             int64_t count, int64_t total_n, int64_t blocksize, const float code[16], int dtype,
+                             void *stream);
+
 /* ------------------------------------------------------------ segments
  *
  * The memory-bound code between the block linears (selas/models/flux.py:
@@ -121,7 +149,7 @@ int selas_gated_add_mod(const float *x, int64_t B, int64_t L, int64_t D, int64_t
 /* Single-stream attention prep: qkv [B, L, 3*H*Dh] (channel = which*H*Dh + h*Dh + d,
  * strides qkv_sb, qkv_sl) -> q, k = dtype(RoPE(RMSNorm(.) * scale)), v = copy,
  * each [B, H, L, Dh] contiguous. RMSNorm eps 1e-6 over Dh in fp32; RoPE rotates
- * interleaved pairs with cos/sin [L, Dh/2] fp32. Dh must be 128.
+ * interleaved pairs with cos/sin [L, Dh/2] fp32. Dh must be even and at most 128.
  * Replaces _qkv_single (flux.py:188-191) with _heads, qk_rms, apply_rope (117-132). */
 int selas_qkv_single(const void *qkv, int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t qkv_sb,
                      int64_t qkv_sl, const float *q_scale, const float *k_scale, const float *cos,

@@ -28,6 +28,7 @@ SIGNATURES: dict[str, list] = {
     "selas_nf4_dequant": [_P, _P, _I64, _I64, _F16x, _P, _INT, _P],
     "selas_nf4_encode": [_P, _I64, _I64, _F16x, _P, _P, _P],
     "selas_nf4_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _F16x, _I64, _P, _P, _I64, _INT, _P],
+    "selas_nf4_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F16x, _INT, _P],
     "selas_mod_in": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _INT, _P],
     "selas_gated_add": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P],
     "selas_gated_add_mod": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P, _I64,

@@ -52,9 +52,65 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 
 // =========================================================================== GEMV (M <= 32)
 
+// The skinny kernels multiply x by codes and apply the block absmax to the
+// fp32 block sums. A code c is fed to the MFMA as two bf16 terms hi + lo with
+// hi = bf16(c) and lo = bf16(c - hi) (|c - hi - lo| <= 2^-17 |c|): with hi
+// alone, the fixed rounding error of each code would add up coherently over K
+// for inputs with a nonzero mean. Two LDS tables map a packed byte to the bf16
+// pair (code of the high nibble, code of the low nibble): hi terms in the
+// first, lo terms in the second, each with kSplitRepl replicas so that the
+// lanes of a ds_read_b32 spread over the banks.
+constexpr int kSplitRepl = 32;
+constexpr int kSplitTableWords = 2 * 256 * kSplitRepl;
+
+// Builds both tables with nthreads threads (a multiple of 256); each lane
+// writes its replicas in a rotated order so that a store touches distinct banks.
+__device__ __forceinline__ void build_split_table(uint32_t *table, const Code16 &code, uint32_t *scratch32,
+                                                  int tid, int nthreads) {
+  if (tid < 16) {
+    const float c = code.v[tid];
+    const uint32_t hi = bf16_bits_rne(c);
+    scratch32[tid] = hi | (static_cast<uint32_t>(bf16_bits_rne(c - bf16_bits_to_f32(hi))) << 16);
+  }
+  __syncthreads();
+  const int b = tid & 255, part = tid >> 8, parts = nthreads >> 8;
+  const uint32_t chi = scratch32[b >> 4], clo = scratch32[b & 15];
+  const uint32_t vhi = (chi & 0xffffu) | (clo << 16), vlo = (chi >> 16) | (clo & 0xffff0000u);
+  const int per = kSplitRepl / parts, lane = tid & 63;
+  for (int j = 0; j < per; ++j) {
+    const int r = (per * part + j + lane) & (kSplitRepl - 1);
+    table[b * kSplitRepl + r] = vhi;
+    table[256 * kSplitRepl + b * kSplitRepl + r] = vlo;
+  }
+}
+
+// hi and lo bf16 operand fragments for the eight codes of packed dword P.
+// lane_hi = lane % 32; lane_lo = lane % 32 + (offset of the lo table), made
+// opaque once so that the compiler keeps the hi and lo reads separate (merged
+// into one two-address read they would land interleaved and need moves).
+struct CodeFrags {
+  uint4 hi, lo;
+};
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ CodeFrags lookup_codes(const uint32_t *table, uint32_t P, uint32_t lane_hi,
+                                                  uint32_t lane_lo) {
+  const uint32_t b0 = (P & 0xffu) * kSplitRepl, b1 = ((P >> 8) & 0xffu) * kSplitRepl;
+  const uint32_t b2 = ((P >> 16) & 0xffu) * kSplitRepl, b3 = (P >> 24) * kSplitRepl;
+  CodeFrags f;
+  f.hi = make_uint4(table[b0 + lane_hi], table[b1 + lane_hi], table[b2 + lane_hi], table[b3 + lane_hi]);
+  f.lo = make_uint4(table[b0 + lane_lo], table[b1 + lane_lo], table[b2 + lane_lo], table[b3 + lane_lo]);
+  return f;
+}
+__device__ __forceinline__ f32x16 mfma_codes(const CodeFrags &f, bf16x8 xf, f32x16 p) {
+  p = mfma32(xf, __builtin_bit_cast(bf16x8, f.hi), p);
+  return mfma32(xf, __builtin_bit_cast(bf16x8, f.lo), p);
+}
+
 constexpr int kGemvThreads = 256;
-constexpr int kGemvGroups = 2;     // 32-column groups per workgroup
-constexpr int kGemvRepl = 64;      // LDS table replicas (one per lane: conflict-free)
+constexpr int kGemvGroups = 2;  // 32-column groups per workgroup
 
 // Workgroup: 64 output columns, all M (<= 32) rows. The four waves split the
 // K blocks round-robin (wave w takes blocks w, w+4, ...) and their fp32
@@ -64,27 +120,14 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, int M, int K, const uint8_t *__restrict__ packed,
     const float *__restrict__ absmax, Code16 code, int N, const uint16_t *__restrict__ bias,
     uint16_t *__restrict__ y, int64_t ldy) {
-  extern __shared__ uint32_t lds[];  // [256 byte values][kGemvRepl] bf16 pairs; later the reduction buffer
+  extern __shared__ uint32_t lds[];  // split code table; later the reduction buffer
+  __shared__ uint32_t codes[16];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c = lane & 31;
-
-  {  // byte b -> (bf16(code[b >> 4]) low, bf16(code[b & 15]) high), replicated per lane
-    uint32_t cb[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) cb[i] = bf16_bits_rne(code.v[i]);
-    for (int e = tid; e < 256 * kGemvRepl; e += kGemvThreads) {
-      const int b = e / kGemvRepl;
-      uint32_t hi = 0, lo = 0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        hi = (b >> 4) == i ? cb[i] : hi;
-        lo = (b & 15) == i ? cb[i] : lo;
-      }
-      lds[e] = hi | (lo << 16);
-    }
-  }
+  build_split_table(lds, code, codes, tid, kGemvThreads);
   __syncthreads();
+  const uint32_t lane_lo = opaque_u32(static_cast<uint32_t>(c) + 256 * kSplitRepl);
 
   const int kblocks = K >> 6;
   const int n_base = blockIdx.x * (32 * kGemvGroups);
@@ -97,7 +140,6 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
     wr[g] = packed + n * (K >> 1) + 16 * h;
     ar[g] = absmax + n * kblocks;
   }
-  const uint32_t lane_off = static_cast<uint32_t>(lane);
 
   f32x16 acc[kGemvGroups];
 #pragma unroll
@@ -117,17 +159,12 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
 #pragma unroll
     for (int g = 0; g < kGemvGroups; ++g) {
       const uint32_t words[4] = {wq[g].x, wq[g].y, wq[g].z, wq[g].w};
+      CodeFrags f[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) f[s] = lookup_codes(lds, words[s], c, lane_lo);
       f32x16 p = f32x16{};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint32_t P = words[s];
-        uint4 t;
-        t.x = lds[((P & 0xffu) * kGemvRepl) + lane_off];
-        t.y = lds[(((P >> 8) & 0xffu) * kGemvRepl) + lane_off];
-        t.z = lds[(((P >> 16) & 0xffu) * kGemvRepl) + lane_off];
-        t.w = lds[((P >> 24) * kGemvRepl) + lane_off];
-        p = mfma32(xf[s], __builtin_bit_cast(bf16x8, t), p);
-      }
+      for (int s = 0; s < 4; ++s) p = mfma_codes(f[s], xf[s], p);
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[g][r] += p[r] * a[g];
     }
@@ -154,11 +191,185 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
   }
 }
 
+// ------------------------------------------------------------- persistent skinny GEMM
+//
+// For M <= 32 and K <= 3072 (the hoisted modulation linears: K = hidden).
+// One 512-thread workgroup per CU. The eight waves split the K blocks
+// (wave w takes blocks w, w+8, ...) and keep their share of x in registers for
+// the whole launch, so x is read once per workgroup. The workgroup then
+// streams 32-row slabs ("units") of one or many weights: each wave multiplies
+// its K share of the slab while the next slab's codes are already loading,
+// the eight partial results are summed in LDS in wave order (deterministic;
+// two alternating buffers, one barrier per unit), bias is added and the bf16
+// result stored.
+
+constexpr int kPgThreads = 512, kPgWaves = 8, kPgRows = 32;
+constexpr int kPgMaxKb = 6;  // K blocks per wave: K <= 8 * 6 * 64 = 3072
+constexpr int kPgTableWords = kSplitTableWords;
+constexpr int kPgRedWords = 2 * kPgWaves * 16 * 64;  // two buffers of [wave][r][lane] partial sums
+constexpr int kPgMaxDescs = 1024;
+
+struct GemvDesc {
+  const uint8_t *packed;
+  const float *absmax;
+  const uint16_t *bias;
+  uint16_t *y;
+  int64_t n;
+  int64_t ldy;
+};
+
+__global__ __launch_bounds__(kPgThreads, 1) void nf4_gemv_persistent(
+    const uint16_t *__restrict__ x, int64_t ldx, int M, int K, const GemvDesc *__restrict__ descs, int count,
+    GemvDesc one, Code16 code) {
+  extern __shared__ uint32_t lds[];
+  uint32_t *table = lds;                                                    // split code table
+  float *red = reinterpret_cast<float *>(lds + kPgTableWords);               // [buf][wave][r][lane]
+  int *prefix = reinterpret_cast<int *>(lds + kPgTableWords + kPgRedWords);  // units before weight g
+  __shared__ uint32_t codes[16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c = lane & 31;
+
+  if (tid == 0) {
+    int acc = 0;
+    for (int g = 0; g < count; ++g) {
+      prefix[g] = acc;
+      const int64_t n = descs ? descs[g].n : one.n;
+      acc += static_cast<int>((n + kPgRows - 1) / kPgRows);
+    }
+    prefix[count] = acc;
+  }
+  build_split_table(table, code, codes, tid, kPgThreads);
+  const uint32_t lane_lo = opaque_u32(static_cast<uint32_t>(c) + 256 * kSplitRepl);
+
+  // This wave's share of x: blocks kb = wave + 8*i; fragment s of a block holds
+  // x[row][64*kb + 32*h + 8*s .. +8] with row = lane % 32 (rows past M repeat row M-1).
+  const int kblocks = K >> 6;
+  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 32 * h;
+  bf16x8 xf[kPgMaxKb][4];
+#pragma unroll
+  for (int i = 0; i < kPgMaxKb; ++i) {
+    const int kb = wave + kPgWaves * i;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      xf[i][s] = kb < kblocks ? *reinterpret_cast<const bf16x8 *>(xr + kb * 64 + 8 * s) : bf16x8{};
+  }
+  __syncthreads();
+
+  const int units_total = prefix[count];
+  const int units_per_wg = (units_total + gridDim.x - 1) / gridDim.x;
+  const int u_begin = blockIdx.x * units_per_wg;
+  const int u_end = min(u_begin + units_per_wg, units_total);
+  // Loads the codes and scales of unit u for this lane (row n of the slab).
+  auto locate = [&](int u, int &g) {
+    while (prefix[g + 1] <= u) ++g;
+  };
+  auto load = [&](int u, int g, uint4 (&wq)[kPgMaxKb], float (&a)[kPgMaxKb]) {
+    const GemvDesc d = descs ? descs[g] : one;
+    const int64_t n = min(static_cast<int64_t>((u - prefix[g]) * kPgRows + c), d.n - 1);
+    const uint8_t *wrow = d.packed + n * (K >> 1) + 16 * h;
+    const float *arow = d.absmax + n * kblocks;
+#pragma unroll
+    for (int i = 0; i < kPgMaxKb; ++i) {
+      const int kb = wave + kPgWaves * i;
+      if (kb < kblocks) {
+        wq[i] = *reinterpret_cast<const uint4 *>(wrow + kb * 32);
+        a[i] = arow[kb];
+      }
+    }
+  };
+  auto unit = [&](int u, int g, const uint4 (&wq)[kPgMaxKb], const float (&a)[kPgMaxKb], int buf) {
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int i = 0; i < kPgMaxKb; ++i) {
+      if (wave + kPgWaves * i >= kblocks) continue;
+      const uint32_t words[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+      CodeFrags f[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) f[s] = lookup_codes(table, words[s], c, lane_lo);
+      f32x16 p = f32x16{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) p = mfma_codes(f[s], xf[i][s], p);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += p[r] * a[i];
+    }
+    float *rb = red + buf * (kPgWaves * 16 * 64);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rb[(wave * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();  // also: everyone finished reading this buffer two units ago
+    const GemvDesc d = descs ? descs[g] : one;
+    const int N = static_cast<int>(d.n);
+    const int n_base = (u - prefix[g]) * kPgRows;
+    for (int e = tid; e < 16 * 64; e += kPgThreads) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kPgWaves; ++w) v += rb[w * 1024 + e];
+      const int l = e & 63, r = e >> 6;
+      const int m = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      const int n = n_base + (l & 31);
+      if (m < M && n < N) {
+        const float b = d.bias ? bf16_bits_to_f32(d.bias[n]) : 0.0f;
+        d.y[static_cast<int64_t>(m) * d.ldy + n] = bf16_bits_rne(v + b);
+      }
+    }
+  };
+
+  // Two register sets: unit u computes from one while unit u+1 loads into the other.
+  uint4 wq0[kPgMaxKb], wq1[kPgMaxKb];
+  float a0[kPgMaxKb], a1[kPgMaxKb];
+  int g = 0, g1 = 0;
+  if (u_begin < u_end) {
+    locate(u_begin, g);
+    load(u_begin, g, wq0, a0);
+  }
+  for (int u = u_begin; u < u_end; u += 2) {
+    g1 = g;
+    if (u + 1 < u_end) {
+      locate(u + 1, g1);
+      load(u + 1, g1, wq1, a1);
+    }
+    unit(u, g, wq0, a0, 0);
+    if (u + 1 >= u_end) break;
+    g = g1;
+    if (u + 2 < u_end) {
+      locate(u + 2, g);
+      load(u + 2, g, wq0, a0);
+    }
+    unit(u + 1, g1, wq1, a1, 1);
+  }
+}
+
+int cu_count() {
+  static int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    return v;
+  }();
+  return n;
+}
+
+// total_n: sum of the weights' row counts (an upper bound on the work, for the grid size).
+int launch_gemv_persistent(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const GemvDesc *descs, int count,
+                           const GemvDesc &one, int64_t total_n, const Code16 &c, hipStream_t s) {
+  const int64_t units = cdiv(total_n, kPgRows) + count;
+  const int64_t wgs_max = cu_count();
+  const int64_t grid = min(units, wgs_max);
+  const size_t lds = (kPgTableWords + kPgRedWords + count + 1) * sizeof(uint32_t);
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_gemv_persistent),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (kPgTableWords + kPgRedWords + kPgMaxDescs + 1) * 4);
+  if (attr != hipSuccess)
+    return set_error(SELAS_EHIP, "nf4_linear: cannot reserve %d bytes of LDS: %s",
+                     (kPgTableWords + kPgRedWords + kPgMaxDescs + 1) * 4, hipGetErrorString(attr));
+  nf4_gemv_persistent<<<dim3(static_cast<uint32_t>(grid)), dim3(kPgThreads), lds, s>>>(
+      x, ldx, static_cast<int>(M), static_cast<int>(K), descs, count, one, c);
+  return check_launch("nf4_linear (persistent gemv)");
+}
+
 // =========================================================================== GEMM (M > 32)
 
-constexpr int kBM = 256, kBN = 256;
 constexpr int kGemmThreads = 256;
-constexpr int kATileBytes = kBM * 128;  // 256 rows x 64 bf16
 
 // 16 bf16(code[i] * a) values as four byte planes (TL = low bytes, TH = high
 // bytes), entries 4j..4j+3 in plane register j. Lanes l and l+32 serve the
@@ -216,127 +427,222 @@ __device__ __forceinline__ bf16x8 dequant8(const Tables &t, uint32_t P) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// s_waitcnt with only the vector-memory counter limited to N (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// LDS reads done, then a workgroup barrier; a compiler fence for LDS accesses.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 16 bytes per lane from a buffer straight into LDS: lane i writes lds + 16*i.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+}
+
+// Interleaving of one sub-step: after each of the N MFMAs, V VALU
+// instructions, and one LDS read after every R-th MFMA.
+template <int N, int R, int V>
+__device__ __forceinline__ void interleave_substep() {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
+    if (i % R == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x002, V, 0);                // VALU
+  }
+}
+
+// Fused-dequant GEMM. A workgroup is 4 waves side by side along N; a wave owns
+// MB*32 rows x CB*32 columns of the output (MB*CB = 16 tiles of 32x32, 256
+// accumulator registers):
+//   MB=16, CB=1: 512 x 128 tile; each decoded weight serves 512 rows, which
+//                halves the decode work per MFMA; 2 LDS stages of 64 KiB.
+//   MB=8,  CB=2: 256 x 256 tile for small M; 3 LDS stages of 32 KiB.
+//
+// Grid: workgroup b runs on XCD b % 8; tile t = (b % 8) * per_xcd + b / 8
+// gives each XCD a contiguous range of tiles, column tile fastest, so that
+// the workgroups an XCD runs at once share one row slab of x in its L2.
+//
+// Pipeline per 64-wide K block kb (LDS stage kb % STAGES):
+//   * the x tile of block kb+STAGES-1 is loaded by buffer->LDS DMA and its
+//     packed codes / absmax into registers, STAGES-1 blocks ahead;
+//   * sub-step s runs the MFMAs for k-slice s; after each MFMA the register
+//     that held its x fragment is refilled with the next sub-step's fragment,
+//     and the next sub-step's weight fragments are decoded in between;
+//   * before sub-step 3 the block kb+1 loads are waited for and the
+//     workgroup synchronises; sub-step 3 then overlaps with building the
+//     product tables and first fragments of block kb+1.
+template <int MB, int CB, int STAGES>
 __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
     const uint16_t *__restrict__ X, int64_t ldx, int M, int K, const uint8_t *__restrict__ packed,
     const float *__restrict__ absmax, Code16 code, int N, const uint16_t *__restrict__ bias,
-    uint16_t *__restrict__ Y, int64_t ldy, int tiles_m) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kATileBytes];
+    uint16_t *__restrict__ Y, int64_t ldy, int tiles_n, int tiles, int per_xcd) {
+  constexpr int TM = 32 * MB, WN = 32 * CB, TN = 4 * WN;
+  constexpr int SB = TM * 128;  // bytes of one x stage: TM rows x 64 bf16
+  constexpr int LOOK = STAGES - 1;
+  constexpr int LPB = 2 * CB + MB;  // vector-memory loads issued per K block and wave
+  static_assert(MB * CB == 16 && (STAGES == 2 || STAGES == 3), "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB];
+  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (t >= tiles) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c = lane & 31;
-  const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
-  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int tm = t / tiles_n, tn = t - tm * tiles_n;
+  const int m0 = tm * TM, n0 = tn * TN;
   const int kblocks = K >> 6;
   const uint32_t ldx_b = static_cast<uint32_t>(ldx) * 2u;
 
-  // Buffer resources: loads past the end of a tensor return zeros, so rows
-  // beyond M or N need no clamping (their results are never stored).
+  // Buffer resources; the range check covers the per-lane offset, which holds
+  // the row term, so rows past M or N read as zeros (never stored).
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(X, static_cast<uint32_t>(M) * ldx_b);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(packed, static_cast<uint32_t>(N) * static_cast<uint32_t>(K >> 1));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(absmax, static_cast<uint32_t>(N) * static_cast<uint32_t>(kblocks) * 4u);
 
-  // x tile loader: thread handles rows (tid>>3) + 32j of the tile, 16-byte chunk tid&7,
-  // stored XOR-swizzled so that the fragment reads below are bank-conflict free.
-  // The hardware range check covers the per-lane offset only, so the row term
-  // lives there: rows >= M are out of range and read as zeros.
-  const int a_row0 = tid >> 3, a_chunk = tid & 7;
-  const uint32_t a_voff = static_cast<uint32_t>(m0 + a_row0) * ldx_b + a_chunk * 16u;
-  const uint32_t a_wr = a_row0 * 128 + ((a_chunk ^ (a_row0 & 7)) << 4);
-  const uint32_t a_jstride = 32u * ldx_b;
-  // Weight rows of this wave: n0 + 64*wave + 32*cb + c.
-  uint32_t b_voff[2], s_voff[2];
+  // x tile DMA: wave w fills tile rows [8*MB*w, 8*MB*(w+1)) with MB loads of 8
+  // rows; lane i of load j lands at row r = 8*MB*w + 8j + i/8, physical
+  // 16-byte chunk i%8, and so fetches logical chunk (i%8) ^ ((r/2)%8). With
+  // that swizzle the 16 lanes one LDS cycle serves in a fragment read (16
+  // consecutive rows, one logical chunk) hit 16 distinct 4-bank groups of the
+  // 64 banks. (r/2)%8 = (4j + i/16) % 8 depends on j only through its parity.
+  uint32_t a_voff[2];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const uint32_t n = static_cast<uint32_t>(n0 + 64 * wave + 32 * cb + c);
+  for (int par = 0; par < 2; ++par)
+    a_voff[par] = static_cast<uint32_t>(m0 + 8 * MB * wave + (lane >> 3)) * ldx_b +
+                  (static_cast<uint32_t>((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 4);
+  const uint32_t a_vstep = 8u * ldx_b;
+  uint8_t *const a_dst = smem + wave * MB * 1024;
+  // Weight rows of this wave: n0 + WN*wave + 32*cb + c.
+  uint32_t b_voff[CB], s_voff[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const uint32_t n = static_cast<uint32_t>(n0 + WN * wave + 32 * cb + c);
     b_voff[cb] = n * static_cast<uint32_t>(K >> 1) + 16u * h;
     s_voff[cb] = n * static_cast<uint32_t>(kblocks) * 4u;
   }
   float cl[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) cl[i] = h ? code.v[8 + i] : code.v[i];
-  // LDS offset of the x fragment for sub-step s (row c of each 32-row slab mb,
-  // slab mb adds mb*4096).
+  // LDS offset of this lane's x fragment for sub-step s (row slab mb adds mb*4096).
   uint32_t a_rd[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) a_rd[s] = c * 128 + (((4 * h + s) ^ (c & 7)) << 4);
+  for (int s = 0; s < 4; ++s) a_rd[s] = c * 128 + (((4 * h + s) ^ ((c >> 1) & 7)) << 4);
 
-  f32x16 acc[8][2];
+  // Loads block `blk` into LDS stage `stage` and the registers bq/bs; the
+  // register loads go first so that later uses of them do not wait for the DMA.
+  auto issue = [&](int stage, int blk, uint4 (&bq)[CB], float (&bs)[CB]) {
+    const uint32_t kb = static_cast<uint32_t>(blk);
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = f32x16{};
-
-  uint4 areg[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) areg[j] = load_b128(xr, a_voff + j * a_jstride, 0);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4 *>(smem + a_wr + j * 4096) = areg[j];
-  uint4 bq[2];
-  float bs[2];
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    bq[cb] = load_b128(wr, b_voff[cb], 0);
-    bs[cb] = load_f32(sr, s_voff[cb], 0);
-  }
-  __syncthreads();
-
-  for (int kb = 0; kb < kblocks; ++kb) {
-    const uint32_t buf = (kb & 1) * kATileBytes;
-    const bool more = kb + 1 < kblocks;
-    uint4 bq_next[2];
-    float bs_next[2];
-    if (more) {
-      const uint32_t ka = (kb + 1) * 128u;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) areg[j] = load_b128(xr, a_voff + j * a_jstride, ka);
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        bq_next[cb] = load_b128(wr, b_voff[cb], (kb + 1) * 32u);
-        bs_next[cb] = load_f32(sr, s_voff[cb], (kb + 1) * 4u);
-      }
+    for (int cb = 0; cb < CB; ++cb) {
+      bq[cb] = load_b128(wr, b_voff[cb], kb * 32u);
+      bs[cb] = load_f32(sr, s_voff[cb], kb * 4u);
     }
-    Tables tab[2];
+    uint8_t *dst = a_dst + stage * SB;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) tab[cb] = make_tables(cl, bs[cb]);
+    for (int j = 0; j < MB; ++j) load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
+  };
+  auto frag = [&](int kb, int s, int mb) {
+    return *reinterpret_cast<const bf16x8 *>(smem + (kb % STAGES) * SB + a_rd[s] + mb * 4096);
+  };
+  auto word = [](const uint4 &q, int s) { return s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w; };
+
+  f32x16 acc[MB][CB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[mb][cb] = f32x16{};
+
+  // Every iteration issues the loads of block kb+LOOK; past the last block the
+  // last block is loaded again (valid addresses, into the stage that is free)
+  // so that the loop body has no branches and schedules as one region.
+  uint4 bq0[CB], bq1[CB], bq2[CB];
+  float bs0[CB], bs1[CB], bs2[CB];
+  issue(0, 0, bq0, bs0);
+  if constexpr (STAGES == 3) {
+    issue(1, min(1, kblocks - 1), bq1, bs1);
+    wait_vmcnt<LPB>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  lds_barrier();
+
+  bf16x8 af[MB], wf[2][CB];
+  Tables tab[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    tab[cb] = make_tables(cl, bs0[cb]);
+    wf[0][cb] = dequant8(tab[cb], word(bq0[cb], 0));
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) af[mb] = frag(0, 0, mb);
+
+  // One K block. cq holds block kb's codes, nq/ns block kb+1's, fq/fs receive
+  // block kb+LOOK's (with one block of lookahead that is nq/ns itself). The
+  // loop below is unrolled STAGES times so that the register sets rotate by
+  // name, never by copying registers that a load in flight still targets.
+  auto block = [&](int kb, const uint4 (&cq)[CB], const uint4 (&nq)[CB], const float (&ns)[CB], uint4 (&fq)[CB],
+                   float (&fs)[CB]) {
+    issue((kb + LOOK) % STAGES, min(kb + LOOK, kblocks - 1), fq, fs);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      bf16x8 wf[2];
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s < 3) {
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const uint32_t P = s == 0 ? bq[cb].x : s == 1 ? bq[cb].y : s == 2 ? bq[cb].z : bq[cb].w;
-        wf[cb] = dequant8(tab[cb], P);
+        for (int cb = 0; cb < CB; ++cb) wf[nxt][cb] = dequant8(tab[cb], word(cq[cb], s + 1));
+      } else {
+        wait_vmcnt<(LOOK - 1) * LPB>();
+        lds_barrier();
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          tab[cb] = make_tables(cl, ns[cb]);
+          wf[nxt][cb] = dequant8(tab[cb], word(nq[cb], 0));
+        }
       }
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        const bf16x8 xf = *reinterpret_cast<const bf16x8 *>(smem + buf + a_rd[s] + mb * 4096);
+      for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = mfma32(wf[cb], xf, acc[mb][cb]);
+        for (int cb = 0; cb < CB; ++cb) acc[mb][cb] = mfma32(wf[cur][cb], af[mb], acc[mb][cb]);
+        af[mb] = s < 3 ? frag(kb, s + 1, mb) : frag(kb + 1, 0, mb);
       }
+      if (s < 3) interleave_substep<MB * CB, CB, (26 * CB + 15) / 16 + 1>();
+      else interleave_substep<MB * CB, CB, (50 * CB + 15) / 16 + 1>();
     }
-    if (more) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4 *>(smem + (kATileBytes - buf) + a_wr + j * 4096) = areg[j];
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        bq[cb] = bq_next[cb];
-        bs[cb] = bs_next[cb];
-      }
-    }
-    __syncthreads();
-  }
+  };
 
-  // Epilogue: acc[mb][cb] holds D[n][m] for n = n0 + 64*wave + 32*cb + 8*(r/4) + 4*h + r%4
+  int kb = 0;
+  if constexpr (STAGES == 3) {
+    for (; kb + 3 <= kblocks; kb += 3) {
+      block(kb, bq0, bq1, bs1, bq2, bs2);
+      block(kb + 1, bq1, bq2, bs2, bq0, bs0);
+      block(kb + 2, bq2, bq0, bs0, bq1, bs1);
+    }
+    if (kb < kblocks) block(kb, bq0, bq1, bs1, bq2, bs2);
+    if (kb + 1 < kblocks) block(kb + 1, bq1, bq2, bs2, bq0, bs0);
+  } else {
+    for (; kb + 2 <= kblocks; kb += 2) {
+      block(kb, bq0, bq1, bs1, bq1, bs1);
+      block(kb + 1, bq1, bq0, bs0, bq0, bs0);
+    }
+    if (kb < kblocks) block(kb, bq0, bq1, bs1, bq1, bs1);
+  }
+  (void)bq2;
+  (void)bs2;
+
+  // Epilogue: acc[mb][cb] holds D[n][m] for n = n0 + WN*wave + 32*cb + 8*(r/4) + 4*h + r%4
   // and m = m0 + 32*mb + c; four consecutive n per r/4 are stored as one 8-byte write.
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
+  for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = n0 + 64 * wave + 32 * cb + 8 * q + 4 * h;
+      const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h;
       float bv[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) bv[t] = (bias && n + t < N) ? bf16_bits_to_f32(bias[n + t]) : 0.0f;
+      for (int t4 = 0; t4 < 4; ++t4) bv[t4] = (bias && n + t4 < N) ? bf16_bits_to_f32(bias[n + t4]) : 0.0f;
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         const int m = m0 + 32 * mb + c;
         if (m >= M) continue;
         uint16_t *dst = Y + static_cast<int64_t>(m) * ldy + n;
@@ -346,11 +652,21 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
           *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
         } else {
           const float v[4] = {v0, v1, v2, v3};
-          for (int t = 0; t < 4 && n + t < N; ++t) dst[t] = bf16_bits_rne(v[t]);
+          for (int t4 = 0; t4 < 4 && n + t4 < N; ++t4) dst[t4] = bf16_bits_rne(v[t4]);
         }
       }
     }
   }
+}
+
+template <int MB, int CB, int STAGES>
+void launch_gemm(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const uint8_t *packed, const float *absmax,
+                 const Code16 &c, int64_t N, const uint16_t *bias, uint16_t *y, int64_t ldy, hipStream_t s) {
+  const int64_t tiles_m = cdiv(M, 32 * MB), tiles_n = cdiv(N, 128 * CB), tiles = tiles_m * tiles_n;
+  const int64_t per_xcd = cdiv(tiles, 8);
+  nf4_gemm_kernel<MB, CB, STAGES><<<dim3(static_cast<uint32_t>(per_xcd * 8)), dim3(kGemmThreads), 0, s>>>(
+      x, ldx, static_cast<int>(M), static_cast<int>(K), packed, absmax, c, static_cast<int>(N), bias, y, ldy,
+      static_cast<int>(tiles_n), static_cast<int>(tiles), static_cast<int>(per_xcd));
 }
 
 }  // namespace
@@ -379,7 +695,7 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
                                          "8-byte aligned y rows");
   // Buffer offsets are 32-bit: every operand (plus one tile of overhang) must span < 4 GiB.
   const int64_t lim = (1ll << 32) - 1;
-  if ((M + 256) * ldx * 2 > lim || (N + 256) * (K / 2) > lim || (N + 256) * (K / 64) * 4 > lim)
+  if ((M + 512) * ldx * 2 > lim || (N + 256) * (K / 2) > lim || (N + 256) * (K / 64) * 4 > lim)
     return set_error(SELAS_EUNSUPPORTED, "nf4_linear: operand above 4 GiB");
   Code16 c;
   for (int i = 0; i < 16; ++i) c.v[i] = code[i];
@@ -387,16 +703,43 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
   const uint16_t *xb = static_cast<const uint16_t *>(x);
   const uint16_t *bb = static_cast<const uint16_t *>(bias);
   uint16_t *yb = static_cast<uint16_t *>(y);
+  if (M <= 32 && K <= kPgWaves * kPgMaxKb * 64) {
+    const GemvDesc one{packed, absmax, bb, yb, N, ldy};
+    return launch_gemv_persistent(xb, ldx, M, K, nullptr, 1, one, N, c, s);
+  }
   if (M <= 32) {
     const int64_t grid = cdiv(N, 32 * kGemvGroups);
-    const size_t lds = 256 * kGemvRepl * sizeof(uint32_t);
+    const size_t lds = kSplitTableWords * sizeof(uint32_t);
     nf4_gemv_kernel<<<dim3(static_cast<uint32_t>(grid)), dim3(kGemvThreads), lds, s>>>(
         xb, ldx, static_cast<int>(M), static_cast<int>(K), packed, absmax, c, static_cast<int>(N), bb, yb, ldy);
     return check_launch("nf4_linear (gemv)");
   }
-  const int64_t tiles_m = cdiv(M, kBM), tiles_n = cdiv(N, kBN);
-  nf4_gemm_kernel<<<dim3(static_cast<uint32_t>(tiles_m * tiles_n)), dim3(kGemmThreads), 0, s>>>(
-      xb, ldx, static_cast<int>(M), static_cast<int>(K), packed, absmax, c, static_cast<int>(N), bb, yb, ldy,
-      static_cast<int>(tiles_m));
+  launch_gemm<8, 2, 3>(xb, ldx, M, K, packed, absmax, c, N, bb, yb, ldy, s);
   return check_launch("nf4_linear (gemm)");
+}
+
+extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx,
+                                        const selas_nf4_gemv_desc *descs, int64_t count, int64_t total_n,
+                                        int64_t blocksize, const float code[16], int dtype, void *stream) {
+  static_assert(sizeof(selas_nf4_gemv_desc) == sizeof(GemvDesc), "descriptor layout");
+  if (M < 0 || K <= 0 || count < 0 || total_n < 0)
+    return set_error(SELAS_EINVAL, "nf4_linear_grouped: bad shape M=%lld K=%lld count=%lld", (long long)M,
+                     (long long)K, (long long)count);
+  if (M == 0 || count == 0) return ok();
+  if (!x || !descs || !code) return set_error(SELAS_EINVAL, "nf4_linear_grouped: null pointer");
+  if (ldx < K) return set_error(SELAS_EINVAL, "nf4_linear_grouped: ldx below K");
+  if (dtype != SELAS_BF16) return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: takes bf16");
+  if (blocksize != 64 || K % 64 || M > 32 || K > kPgWaves * kPgMaxKb * 64 || count > kPgMaxDescs)
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: needs blocksize 64, K %% 64 == 0, K <= %d, M <= 32, "
+                                         "at most %d weights", kPgWaves * kPgMaxKb * 64, kPgMaxDescs);
+  if (!aligned(x, 16) || ldx % 8 || !aligned(descs, 8))
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: x rows must be 16-byte aligned");
+  if (total_n <= 0 || total_n >= (1ll << 36))
+    return set_error(SELAS_EINVAL, "nf4_linear_grouped: total_n must be the sum of the weights' row counts");
+  Code16 c;
+  for (int i = 0; i < 16; ++i) c.v[i] = code[i];
+  const GemvDesc none{nullptr, nullptr, nullptr, nullptr, 0, 0};
+  return launch_gemv_persistent(static_cast<const uint16_t *>(x), ldx, M, K,
+                                reinterpret_cast<const GemvDesc *>(descs), static_cast<int>(count), none,
+                                total_n, c, static_cast<hipStream_t>(stream));
 }

@@ -22,7 +22,7 @@ import torch.nn.functional as F
 
 from .codecs import EncodedTensor, encode_nf4, encode_raw
 from .kernels import FUSED, Kernels
-from .linear import UnitView
+from .linear import UnitView, nf4_linear_grouped
 
 
 @dataclass
@@ -217,16 +217,36 @@ class RandomFlux:
         units = self.doubles + self.singles + self.mods
         return sum(e.nbytes for u in units for e in u.tensors.values() if e.codec == "nf4")
 
-    @torch.no_grad()
-    def modulations(self, sv: torch.Tensor) -> list[torch.Tensor]:
-        """Every block's modulation vectors [S, 1, kD] from silu(vec) [S, 1, D] (flux.py:428-445)."""
-        out = []
+    def mod_prefixes(self) -> list[tuple[UnitView, str]]:
         nd = len(self.doubles)
+        out = []
         for i, u in enumerate(self.mods):
-            if i < nd:
-                out.append(torch.cat((u.linear(sv, "img_mod.lin"), u.linear(sv, "txt_mod.lin")), dim=-1))
+            out += [(u, "img_mod.lin"), (u, "txt_mod.lin")] if i < nd else [(u, "modulation.lin")]
+        return out
+
+    @torch.no_grad()
+    def modulations(self, sv: torch.Tensor, grouped: bool = True) -> list[torch.Tensor]:
+        """Every block's modulation vectors [S, 1, kD] from silu(vec) [S, 1, D] (flux.py:428-445).
+
+        ``grouped`` runs all modulation linears in one launch (same bits as one call per linear)."""
+        pre = self.mod_prefixes()
+        if grouped:
+            ws = []
+            for u, p in pre:
+                e = u.tensors[p + ".weight"]
+                ws.append((e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"], e.shape,
+                           u.get(p + ".bias")))
+            ys = nf4_linear_grouped(sv, ws)
+        else:
+            ys = [u.linear(sv, p) for u, p in pre]
+        out, i = [], 0
+        for j in range(len(self.mods)):
+            if j < len(self.doubles):
+                out.append(torch.cat((ys[i], ys[i + 1]), dim=-1))
+                i += 2
             else:
-                out.append(u.linear(sv, "modulation.lin"))
+                out.append(ys[i])
+                i += 1
         return out
 
     @torch.no_grad()

@@ -59,6 +59,56 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
         return F.linear(x, w, bias)
 
 
+GROUPED_MAX_K = 3072  # the grouped skinny kernel keeps x in registers: K <= 8 waves x 6 blocks x 64
+GROUPED_MAX_M = 32
+
+
+def nf4_linear_grouped(x: torch.Tensor, weights, code=None) -> list[torch.Tensor]:
+    """``[F.linear(x, decode(W_i), b_i) for W_i, b_i in weights]`` in one launch.
+
+    ``weights``: sequence of (packed, absmax, blocksize, code, shape, bias) tuples that
+    share ``x`` [..., K] with at most 32 rows. Each result has the bits ``nf4_linear``
+    gives for that weight alone. This is the hoisted modulation prologue
+    (selas/models/flux.py:428-445): every modulation linear of a model applied to
+    one silu(vec). Shapes the grouped kernel does not cover are run one by one.
+    """
+    weights = list(weights)
+    if not weights:
+        return []
+    k = x.shape[-1]
+    dev = _lib.require_gpu(x, *(w[0] for w in weights))
+    x2 = _rows(x)
+    m = x2.shape[0]
+    ok = (x.dtype == torch.bfloat16 and m <= GROUPED_MAX_M and k % 64 == 0 and k <= GROUPED_MAX_K
+          and x2.data_ptr() % 16 == 0 and x2.stride(0) % 8 == 0
+          and all(int(w[2]) == 64 and len(w[4]) == 2 and int(w[4][1]) == k for w in weights))
+    if not ok:
+        return [nf4_linear(x, *w) for w in weights]
+    codes = {tuple(float(c) for c in w[3]) for w in weights}
+    if len(codes) != 1:
+        return [nf4_linear(x, *w) for w in weights]
+    outs, rows, total_n = [], [], 0
+    converted = []  # converted biases stay referenced until the launch is queued
+    for packed, absmax, _, _, shape, bias in weights:
+        n = int(shape[0])
+        if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
+            bias = bias.to(x.dtype).contiguous()
+            converted.append(bias)
+        y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+        outs.append(y)
+        rows.append([packed.data_ptr(), absmax.data_ptr(), 0 if bias is None else bias.data_ptr(), y.data_ptr(),
+                     n, n])
+        total_n += n
+    desc = torch.tensor(rows, dtype=torch.int64).to(dev, non_blocking=False)
+    with torch.cuda.device(dev):
+        _lib.call("selas_nf4_linear_grouped", x2.data_ptr(), m, k, x2.stride(0), desc.data_ptr(), len(weights), total_n,
+                  64, _lib.code_array(next(iter(codes))), _lib.BF16, _lib.stream(dev))
+    # desc and converted biases may be freed now: the caching allocator hands their memory only to
+    # later work on this same stream, which runs after the launch.
+    del converted
+    return outs
+
+
 class UnitView:
     """Typed access to one unit's tensors, as selas.store.UnitView (store.py:242-293).
 

@@ -141,3 +141,22 @@ def test_full_size_single_linear(dev):
     rows = torch.randint(0, m, (64,), generator=seeded(2))
     check_close(y[rows], oracle_linear(x[rows], w_ref))
     assert torch.isfinite(y).all()
+
+
+def test_grouped_skinny_equals_one_by_one(dev):
+    from selas_amd.linear import nf4_linear_grouped
+
+    shapes = [(3072 * 6, 3072), (192, 3072), (64, 3072), (100, 3072), (3072 * 3, 3072)]
+    ws = []
+    for i, (n, k) in enumerate(shapes):
+        p, a, w_ref = make_weight(n, k, 40 + i, dev)
+        b = (torch.randn(n, generator=seeded(50 + i)) * 0.02).to(torch.bfloat16).to(dev) if i % 2 == 0 else None
+        ws.append(((p, a, 64, codecs.NF4_CODE, (n, k), b), w_ref))
+    for m in (1, 28, 32):
+        x = torch.nn.functional.silu(torch.randn(m, 1, 3072, generator=seeded(m))).to(torch.bfloat16).to(dev)
+        ys = nf4_linear_grouped(x, [w for w, _ in ws])
+        for (w, w_ref), y in zip(ws, ys):
+            alone = nf4_linear(x, *w)
+            assert y.shape == alone.shape == (m, 1, w[4][0])
+            assert torch.equal(y, alone)  # same bits as the per-linear call
+            check_close(y.reshape(m, -1), oracle_linear(x.reshape(m, -1), w_ref, w[5]))

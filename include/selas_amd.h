@@ -53,7 +53,7 @@ int selas_abi_version(void);
  * NF4 decode: out[2i]   = dtype(code[packed[i] >> 4] * absmax[i / (blocksize/2)])
  *             out[2i+1] = dtype(code[packed[i] & 15] * absmax[i / (blocksize/2)])
  * The fp32 product is rounded once, to nearest even, to out_dtype; the bits
- * equal the reference decode for every input, NaN included.
+ * equal the reference decode for every input except NaN payloads.
  * Replaces nf4_dequant / nf4_dequant_torch (selas/codecs.py:178-199, 260-266)
  * and the Triton kernel (codecs.py:207-228).
  */
@@ -79,8 +79,13 @@ int selas_nf4_encode(const float *w, int64_t n, int64_t blocksize, const float c
  *   bias  [N]     dtype or NULL
  *   y     [M, N]  dtype, row stride ldy
  * dtype is SELAS_BF16 (fp32 accumulation, one rounding of acc + bias).
- * M <= 32 runs a skinny dequant-GEMM, larger M a tiled MFMA GEMM with the
- * dequantization fused into the operand load. Returns SELAS_EUNSUPPORTED
+ * M > 32 runs a tiled MFMA GEMM with the dequantization fused into the operand
+ * load; its operand is the reference's decoded weight bf16(code*absmax) bit for
+ * bit. M <= 32 runs a skinny dequant-GEMM that multiplies x by the codes and
+ * scales the fp32 block sums by absmax (for K = 1024, 2048, 3072 in fp16 after
+ * an exact power-of-two rescale of each row of x; otherwise in bf16 with codes
+ * split into two bf16 terms); it agrees with the decoded-weight product to the
+ * rounding of the decoded weight. Returns SELAS_EUNSUPPORTED
  * when the shape or layout is outside the fused kernels (blocksize != 64,
  * K % 64 != 0, misaligned rows, dtype other than bf16); the caller then
  * decodes with selas_nf4_dequant and uses a library GEMM.
@@ -106,8 +111,9 @@ typedef struct selas_nf4_gemv_desc {
 } selas_nf4_gemv_desc;
 
 /*
- * `count` quantized linears that share one input x [M, K] (M <= 32, K <= 3072,
- * K % 64 == 0, blocksize 64, bf16), computed by one launch: y_i = x W_i^T + b_i.
+ * `count` quantized linears that share one input x [M, K] (M <= 32, K = 1024,
+ * 2048 or 3072, blocksize 64, bf16, at most 1023 weights, 16-byte aligned codes),
+ * computed by one launch: y_i = x W_i^T + b_i.
  * `descs` is a device array of `count` descriptors and total_n the sum of
  * their n (it sizes the launch). Each output has the bits selas_nf4_linear
  * gives for that weight alone.

@@ -4,16 +4,16 @@
 // decodes the whole weight to a bf16 temporary (selas/codecs.py:269-280) and
 // calls F.linear. Here the weight never exists in bf16 outside registers.
 //
-// Two kernels, chosen from M alone:
-//   * M <= 32  (hoisted adaLN modulation linears, M = number of steps):
-//     nf4_gemv_kernel, HBM-bound. Weight codes are looked up as bf16(code)
-//     pairs from a bank-replicated LDS table (one LDS read per byte, no bank
-//     conflicts), multiplied with x on MFMA per 64-element block, and the
-//     block's fp32 absmax is applied to the fp32 block partial sum.
-//   * M > 32 (block linears, M = tokens): nf4_gemm_kernel, MFMA-bound.
+// Kernels, chosen from M and K:
+//   * M <= 32 (hoisted adaLN modulation linears, M = number of steps), HBM-bound:
+//     nf4_gemv_stream for K = 1024, 2048, 3072 (one launch can cover many
+//     weights), nf4_gemv_kernel for other K. Both multiply x by the codes on
+//     MFMA and apply the block's fp32 absmax to the fp32 block partial sums;
+//     codes come from bank-replicated LDS tables indexed by the packed byte.
+//   * M > 32 (block linears, M = tokens), MFMA-bound: nf4_gemm_kernel.
 //     256x256 output tile per workgroup, 4 waves, each wave owns 64 output
-//     columns for all 256 rows. x tiles are staged through LDS (double
-//     buffered, XOR-swizzled 16-byte chunks); weight codes go straight from
+//     columns for all 256 rows. x tiles are staged through LDS (XOR-swizzled
+//     16-byte chunks, three stages in flight); weight codes go straight from
 //     HBM to registers and are decoded to the bit-exact reference operand
 //     bf16(code[nibble] * absmax) with a per-block 16-entry product table and
 //     v_perm_b32 byte lookups, then fed to v_mfma_f32_32x32x16_bf16.
@@ -48,6 +48,14 @@ __device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t vof
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter limited to N (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // =========================================================================== GEMV (M <= 32)
@@ -191,23 +199,61 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
   }
 }
 
-// ------------------------------------------------------------- persistent skinny GEMM
+// ------------------------------------------------------------- streaming skinny GEMM
 //
-// For M <= 32 and K <= 3072 (the hoisted modulation linears: K = hidden).
-// One 512-thread workgroup per CU. The eight waves split the K blocks
-// (wave w takes blocks w, w+8, ...) and keep their share of x in registers for
-// the whole launch, so x is read once per workgroup. The workgroup then
-// streams 32-row slabs ("units") of one or many weights: each wave multiplies
-// its K share of the slab while the next slab's codes are already loading,
-// the eight partial results are summed in LDS in wave order (deterministic;
-// two alternating buffers, one barrier per unit), bias is added and the bf16
-// result stored.
+// For M <= 32 and K = 512 * BPW (BPW = 2, 4, 6: K = 1024, 2048, 3072; the
+// hoisted modulation linears have K = hidden = 3072). One 512-thread
+// workgroup per CU streams 32-row slabs ("units") of one or many weights.
+//
+//   * Wave w owns the K slice of blocks [w*BPW, (w+1)*BPW) and keeps x for that
+//     slice in registers for the whole launch (A fragments, rows past M repeat
+//     row M-1).
+//   * Each wave copies its slice of the unit's codes (32 rows x BPW*32 bytes)
+//     from HBM into its own LDS stage with buffer-load-to-LDS DMA; the unit's
+//     scales (32 rows x K/64 floats, one contiguous block) are copied by the
+//     first BPW waves into a shared double buffer. Consecutive lanes fetch
+//     consecutive 16-byte chunks, so every request covers whole cache lines;
+//     the chunk order inside a code row is XOR-swizzled so that the MFMA-order
+//     reads (lane (c, h) reads row c) are free of bank conflicts.
+//   * Once its codes are in registers a wave issues the next unit's DMA and
+//     multiplies: each code byte is looked up in a 32-way replicated LDS table
+//     of (hi, lo) bf16 pairs (one v_perm for the address, one ds_read_b64),
+//     fed to two MFMAs, and the fp32 block sums are scaled by absmax.
+//   * The eight partial results of a unit are summed in LDS in wave order
+//     (deterministic). Every wave drains its DMAs before the barrier that
+//     precedes the partial-sum stores, so after that barrier the next unit's
+//     codes and scales are in LDS for everyone. The sum and the bf16 stores of
+//     unit u run after the DMA of unit u+2 has been issued.
 
-constexpr int kPgThreads = 512, kPgWaves = 8, kPgRows = 32;
-constexpr int kPgMaxKb = 6;  // K blocks per wave: K <= 8 * 6 * 64 = 3072
-constexpr int kPgTableWords = kSplitTableWords;
-constexpr int kPgRedWords = 2 * kPgWaves * 16 * 64;  // two buffers of [wave][r][lane] partial sums
-constexpr int kPgMaxDescs = 1024;
+constexpr int kSgThreads = 512, kSgWaves = 8, kSgRows = 32;
+constexpr int kSgTableBytes = 256 * 64 * 4;            // [byte][lane] -> fp16 code pair
+constexpr int kSgRedBytes = kSgWaves * 16 * 64 * 4;   // [wave][r][lane] partial sums
+constexpr int kSgMaxDescs = 1023;
+#ifndef SG_AHEAD
+#define SG_AHEAD 1
+#endif
+constexpr int kSgAhead = SG_AHEAD;  // sub-steps of table lookups in flight
+#ifndef SG_SPREAD
+#define SG_SPREAD 0
+#endif
+constexpr bool kSgSpread = SG_SPREAD;  // DMA instructions spread over the compute blocks
+
+template <int BPW>
+struct SgLayout {
+  // A wave's slice of a code row is kChunks 16-byte chunks; the 32 rows of a unit
+  // are kCodeInstrs DMA instructions of 64 chunks.
+  static constexpr int kChunks = 2 * BPW;
+  static constexpr int kCodeInstrs = BPW;
+  static constexpr int kCodeBytes = kSgRows * kChunks * 16;
+  static constexpr int kScaleBytes = kSgRows * 8 * BPW * 4;      // a unit's scales: BPW DMA instructions of 1 KiB
+  static constexpr int kStage = kSgTableBytes;                   // byte offsets in dynamic LDS
+  static constexpr int kScales = kStage + kSgWaves * kCodeBytes;  // two buffers
+  static constexpr int kRed = kScales + 2 * kScaleBytes;
+  static constexpr int kPrefix = kRed + kSgRedBytes;
+  static constexpr int kMaxBytes = kPrefix + (kSgMaxDescs + 1) * 4;
+  static_assert(BPW % 2 == 0 && BPW <= 6, "slice of 2, 4 or 6 blocks per wave");
+  static_assert(kMaxBytes <= 160 * 1024, "LDS");
+};
 
 struct GemvDesc {
   const uint8_t *packed;
@@ -218,125 +264,305 @@ struct GemvDesc {
   int64_t ldy;
 };
 
-__global__ __launch_bounds__(kPgThreads, 1) void nf4_gemv_persistent(
-    const uint16_t *__restrict__ x, int64_t ldx, int M, int K, const GemvDesc *__restrict__ descs, int count,
+// A descriptor held in scalar registers (every field wave-uniform; n and ldy fit 32 bits).
+struct SDesc {
+  const uint8_t *packed;
+  const float *absmax;
+  const uint16_t *bias;
+  uint16_t *y;
+  int n, ldy;
+};
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
+  return reinterpret_cast<T *>(lo | (hi << 32));
+}
+__device__ __forceinline__ SDesc uniform_desc(const GemvDesc &d) {
+  return SDesc{uniform_ptr(d.packed), uniform_ptr(d.absmax), uniform_ptr(d.bias), uniform_ptr(d.y),
+               __builtin_amdgcn_readfirstlane(static_cast<int>(d.n)),
+               __builtin_amdgcn_readfirstlane(static_cast<int>(d.ldy))};
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane i writes lds + 16*i.
+__device__ __forceinline__ void load_lds16_at(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0, 0);
+}
+
+// XOR applied to the chunk index of row r inside a wave's code stage.
+__device__ __forceinline__ int sg_swz(int r) { return (r >> 2) & 3; }
+
+template <int BPW>
+__global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
+    const uint16_t *__restrict__ x, int64_t ldx, int M, const GemvDesc *__restrict__ descs, int count,
     GemvDesc one, Code16 code) {
-  extern __shared__ uint32_t lds[];
-  uint32_t *table = lds;                                                    // split code table
-  float *red = reinterpret_cast<float *>(lds + kPgTableWords);               // [buf][wave][r][lane]
-  int *prefix = reinterpret_cast<int *>(lds + kPgTableWords + kPgRedWords);  // units before weight g
-  __shared__ uint32_t codes[16];
+  using L = SgLayout<BPW>;
+  constexpr int K = 512 * BPW, kblocks = 8 * BPW, row_bytes = K / 2;
+  extern __shared__ __align__(16) uint32_t lds_words[];
+  uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
+  int *prefix = reinterpret_cast<int *>(lds + L::kPrefix);
+  float *red = reinterpret_cast<float *>(lds + L::kRed);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c = lane & 31;
 
-  if (tid == 0) {
-    int acc = 0;
-    for (int g = 0; g < count; ++g) {
-      prefix[g] = acc;
-      const int64_t n = descs ? descs[g].n : one.n;
-      acc += static_cast<int>((n + kPgRows - 1) / kPgRows);
+  // fp16 codebook, staged in the reduction area.
+  uint32_t *code16 = reinterpret_cast<uint32_t *>(red);
+  unsigned *rowmax = reinterpret_cast<unsigned *>(red) + 64;
+  if (tid < 16) code16[tid] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(code.v[tid]));
+  if (tid < 32) rowmax[tid] = 0u;
+  if (wave == 0) {
+    // prefix[g] = units (32-row slabs) before weight g: a wave-wide scan, 64 weights at a time.
+    int carry = 0;
+    for (int base = 0; base < count; base += 64) {
+      const int g = base + lane;
+      int v = 0;
+      if (g < count) v = static_cast<int>(((descs ? descs[g].n : one.n) + kSgRows - 1) / kSgRows);
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(v, off);
+        if (lane >= off) v += t;
+      }
+      if (g < count) prefix[g + 1] = carry + v;
+      carry += __shfl(v, 63);
     }
-    prefix[count] = acc;
-  }
-  build_split_table(table, code, codes, tid, kPgThreads);
-  const uint32_t lane_lo = opaque_u32(static_cast<uint32_t>(c) + 256 * kSplitRepl);
-
-  // This wave's share of x: blocks kb = wave + 8*i; fragment s of a block holds
-  // x[row][64*kb + 32*h + 8*s .. +8] with row = lane % 32 (rows past M repeat row M-1).
-  const int kblocks = K >> 6;
-  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 32 * h;
-  bf16x8 xf[kPgMaxKb][4];
-#pragma unroll
-  for (int i = 0; i < kPgMaxKb; ++i) {
-    const int kb = wave + kPgWaves * i;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      xf[i][s] = kb < kblocks ? *reinterpret_cast<const bf16x8 *>(xr + kb * 64 + 8 * s) : bf16x8{};
+    if (lane == 0) prefix[0] = 0;
   }
   __syncthreads();
+  {
+    // Entry (b, j) at b*256 + 4*j: fp16 pair (code[b >> 4], code[b & 15]), one replica per lane j.
+    const int b = tid & 255, part = tid >> 8;
+    const uint32_t e = code16[b >> 4] | (code16[b & 15] << 16);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int r = 32 * part + ((j + lane) & 31);
+      *reinterpret_cast<uint32_t *>(lds + b * 256 + r * 4) = e;
+    }
+  }
+
+  // x fragments of this wave's slice: block b, sub-step s covers k = 64*(kb0+b) + 32h + 8s .. +8.
+  const int kb0 = wave * BPW;
+  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 64 * kb0 + 32 * h;
+  uint4 xb[BPW][4];
+#pragma unroll
+  for (int b = 0; b < BPW; ++b)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xb[b][s] = *reinterpret_cast<const uint4 *>(xr + 64 * b + 8 * s);
+  // Row maxima of |x| (as bf16 magnitude bits: ordered like the values, NaN above Inf).
+  {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t w[4] = {xb[b][s].x, xb[b][s].y, xb[b][s].z, xb[b][s].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+      }
+    __syncthreads();  // rowmax cleared
+    atomicMax(&rowmax[c], mx);
+  }
+
+  uint8_t *stage = lds + L::kStage + wave * L::kCodeBytes;
+  // MFMA-order reads: lane (c, h) takes chunk 2b + h of row c.
+  const int rd_base = c * L::kChunks * 16, rd_swz = sg_swz(c);
+  // v_perm source for table addresses: byte 0 = 4 * lane, byte 1 <- code byte.
+  const uint32_t tsel = static_cast<uint32_t>(lane) * 4u;
+
+  __syncthreads();  // table, prefix and row maxima ready
+
+  // The skinny kernel multiplies in fp16: each row of x is scaled by a power of
+  // two that brings its largest magnitude into [2^14, 2^15), which makes the
+  // bf16 -> fp16 conversion exact (8 significant bits into 11; values below
+  // 2^-38 of the row maximum fall into fp16 subnormals or to zero), and the
+  // products with the fp16 codebook accumulate in fp32. The output is scaled
+  // back exactly. Rows whose maximum is 0, Inf or NaN keep scale 1.
+  auto row_scale = [&](int row, bool inverse) {
+    const unsigned e = (rowmax[min(row, M - 1)] >> 7) & 0xffu;  // bf16 exponent field of the row maximum
+    if (e == 0u || e == 0xffu) return 1.0f;
+    const int k = 14 - (static_cast<int>(e) - 127);               // scale = 2^k
+    const int kc = max(-126, min(127, inverse ? -k : k));
+    return __uint_as_float(static_cast<uint32_t>(kc + 127) << 23);
+  };
+  f16x8 xf[BPW][4];
+  {
+    const float sc = row_scale(c, false);
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t w[4] = {xb[b][s].x, xb[b][s].y, xb[b][s].z, xb[b][s].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xf[b][s][2 * i] = static_cast<_Float16>(__uint_as_float(w[i] << 16) * sc);
+          xf[b][s][2 * i + 1] = static_cast<_Float16>(__uint_as_float(w[i] & 0xffff0000u) * sc);
+        }
+      }
+  }
+  // Inverse scales of the two output rows this thread finishes (fixed for the launch).
+  float inv_m[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = wave + 8 * i;
+    inv_m[i] = row_scale(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), true);
+  }
 
   const int units_total = prefix[count];
   const int units_per_wg = (units_total + gridDim.x - 1) / gridDim.x;
   const int u_begin = blockIdx.x * units_per_wg;
   const int u_end = min(u_begin + units_per_wg, units_total);
-  // Loads the codes and scales of unit u for this lane (row n of the slab).
-  auto locate = [&](int u, int &g) {
+  if (u_begin >= u_end) return;  // uniform over the workgroup
+
+  auto locate = [&](int u, int g) {
     while (prefix[g + 1] <= u) ++g;
+    return __builtin_amdgcn_readfirstlane(g);
   };
-  auto load = [&](int u, int g, uint4 (&wq)[kPgMaxKb], float (&a)[kPgMaxKb]) {
-    const GemvDesc d = descs ? descs[g] : one;
-    const int64_t n = min(static_cast<int64_t>((u - prefix[g]) * kPgRows + c), d.n - 1);
-    const uint8_t *wrow = d.packed + n * (K >> 1) + 16 * h;
-    const float *arow = d.absmax + n * kblocks;
-#pragma unroll
-    for (int i = 0; i < kPgMaxKb; ++i) {
-      const int kb = wave + kPgWaves * i;
-      if (kb < kblocks) {
-        wq[i] = *reinterpret_cast<const uint4 *>(wrow + kb * 32);
-        a[i] = arow[kb];
-      }
+  // Descriptors are uniform: kept in scalar registers and reloaded only when the weight changes.
+  auto desc = [&](int g) { return uniform_desc(descs ? descs[g] : one); };
+  auto scales = [&](int u) { return reinterpret_cast<float *>(lds + L::kScales + ((u - u_begin) & 1) * L::kScaleBytes); };
+  // DMA instruction j of unit u's codes; j == 0 also fetches this wave's share of the scales.
+  // Code instruction j fetches chunk (p ^ swz(r)) of row r into stage slot
+  // 64j + lane = r*kChunks + p. The buffers start at the unit's first row, so
+  // rows past the weight's end fall outside their ranges and read as 0.
+  auto issue_part = [&](int j, int u, const SDesc &d, int row0) {
+    const uint32_t q = 64u * j + lane, r = q / L::kChunks, p = q - r * L::kChunks;
+    const auto rc = make_rsrc(d.packed + static_cast<int64_t>(row0) * row_bytes,
+                              static_cast<uint32_t>(max(d.n - row0, 0)) * row_bytes);
+    load_lds16_at(rc, stage + 1024 * j, r * row_bytes + 32 * kb0 + 16 * (p ^ sg_swz(r)));
+    if (j == 0 && wave < BPW) {
+      const auto ra = make_rsrc(d.absmax + static_cast<int64_t>(row0) * kblocks,
+                                static_cast<uint32_t>(max(d.n - row0, 0)) * (kblocks * 4));
+      load_lds16_at(ra, reinterpret_cast<uint8_t *>(scales(u)) + 1024 * wave, 1024 * wave + 16 * lane);
     }
   };
-  auto unit = [&](int u, int g, const uint4 (&wq)[kPgMaxKb], const float (&a)[kPgMaxKb], int buf) {
-    f32x16 acc = f32x16{};
+  auto issue = [&](int u, const SDesc &d, int row0) {
 #pragma unroll
-    for (int i = 0; i < kPgMaxKb; ++i) {
-      if (wave + kPgWaves * i >= kblocks) continue;
-      const uint32_t words[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
-      CodeFrags f[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) f[s] = lookup_codes(table, words[s], c, lane_lo);
-      f32x16 p = f32x16{};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) p = mfma_codes(f[s], xf[i][s], p);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] += p[r] * a[i];
-    }
-    float *rb = red + buf * (kPgWaves * 16 * 64);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) rb[(wave * 16 + r) * 64 + lane] = acc[r];
-    __syncthreads();  // also: everyone finished reading this buffer two units ago
-    const GemvDesc d = descs ? descs[g] : one;
-    const int N = static_cast<int>(d.n);
-    const int n_base = (u - prefix[g]) * kPgRows;
-    for (int e = tid; e < 16 * 64; e += kPgThreads) {
+    for (int j = 0; j < L::kCodeInstrs; ++j) issue_part(j, u, d, row0);
+  };
+  // Bias and outputs go through buffer resources, not generic pointers: a
+  // flat access might touch LDS and would make every later LDS read wait for
+  // all outstanding memory operations, the stage DMA included.
+  // Bias bits of the output column this thread stores (loaded one unit ahead).
+  auto load_bias = [&](const SDesc &d, int row0) -> uint32_t {
+    if (!d.bias) return 0u;
+    const int n = min(row0 + c, d.n - 1);
+    const auto rb = make_rsrc(d.bias, static_cast<uint32_t>(d.n * 2));
+    return __builtin_amdgcn_raw_buffer_load_b16(rb, static_cast<uint32_t>(n) * 2u, 0, 0);
+  };
+  // Sum of the eight partials of the unit held in `red`, plus bias, to bf16.
+  // Half i of the outputs of the unit whose partials are in `red`.
+  auto finish = [&](int i, const SDesc &d, int row0, uint32_t bias_bits) {
+    const int N = d.n;
+    const float bv = bf16_bits_to_f32(static_cast<uint16_t>(bias_bits));
+    const auto ry = make_rsrc(d.y, static_cast<uint32_t>(((M - 1) * d.ldy + N) * 2));
+    {
+      const int e = tid + kSgThreads * i;
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kPgWaves; ++w) v += rb[w * 1024 + e];
+      for (int w = 0; w < kSgWaves; ++w) v += red[w * 1024 + e];
       const int l = e & 63, r = e >> 6;
       const int m = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      const int n = n_base + (l & 31);
-      if (m < M && n < N) {
-        const float b = d.bias ? bf16_bits_to_f32(d.bias[n]) : 0.0f;
-        d.y[static_cast<int64_t>(m) * d.ldy + n] = bf16_bits_rne(v + b);
-      }
+      const int n = row0 + (l & 31);
+      if (m < M && n < N)
+        __builtin_amdgcn_raw_buffer_store_b16(bf16_bits_rne(v * inv_m[i] + bv), ry,
+                                              static_cast<uint32_t>(m * d.ldy + n) * 2u, 0, 0);
     }
   };
+  // This wave's codes and scales of unit u, from LDS into registers.
+  uint4 cw[BPW];
+  float a[BPW];
+  auto read_stage = [&](int u) {
+    const float *sc = scales(u) + c * kblocks + kb0;
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+      cw[b] = *reinterpret_cast<const uint4 *>(stage + rd_base + 16 * ((2 * b + h) ^ rd_swz));
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) a[b] = sc[b];
+  };
 
-  // Two register sets: unit u computes from one while unit u+1 loads into the other.
-  uint4 wq0[kPgMaxKb], wq1[kPgMaxKb];
-  float a0[kPgMaxKb], a1[kPgMaxKb];
-  int g = 0, g1 = 0;
-  if (u_begin < u_end) {
-    locate(u_begin, g);
-    load(u_begin, g, wq0, a0);
-  }
-  for (int u = u_begin; u < u_end; u += 2) {
-    g1 = g;
-    if (u + 1 < u_end) {
-      locate(u + 1, g1);
-      load(u + 1, g1, wq1, a1);
+  // Unit u of the loop: weight g_cur (descriptor d_cur, first row row_cur); the
+  // next unit's weight g_nxt. Unit u-1's outputs are finished during unit u.
+  int g_cur = locate(u_begin, 0);
+  SDesc d_cur = desc(g_cur);
+  int row_cur = (u_begin - prefix[g_cur]) * kSgRows;
+  issue(u_begin, d_cur, row_cur);
+  wait_vmcnt<0>();
+  __syncthreads();  // the first unit's codes and scales are in LDS
+  read_stage(u_begin);
+  SDesc d_prev = d_cur;
+  int row_prev = row_cur;
+  uint32_t bias_prev = 0;
+  for (int u = u_begin; u < u_end; ++u) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage read before the next DMA overwrites it
+    const uint32_t bias_cur = load_bias(d_cur, row_cur);
+    int g_nxt = g_cur, row_nxt = row_cur + kSgRows;
+    SDesc d_nxt = d_cur;
+    const bool more = u + 1 < u_end;
+    if (more && row_nxt >= d_cur.n) {
+      g_nxt = locate(u + 1, g_cur);
+      d_nxt = desc(g_nxt);
+      row_nxt = (u + 1 - prefix[g_nxt]) * kSgRows;
     }
-    unit(u, g, wq0, a0, 0);
-    if (u + 1 >= u_end) break;
-    g = g1;
-    if (u + 2 < u_end) {
-      locate(u + 2, g);
-      load(u + 2, g, wq0, a0);
+    if (u > u_begin) {  // partials of unit u-1 (barrier at the end of u-1)
+      finish(0, d_prev, row_prev, bias_prev);
+      finish(1, d_prev, row_prev, bias_prev);
     }
-    unit(u + 1, g1, wq1, a1, 1);
+    if (!kSgSpread && more) issue(u + 1, d_nxt, row_nxt);
+
+    // Table lookups run kSgAhead sub-steps ahead of the MFMAs that use them.
+    auto word = [&](int t) {
+      const uint4 &q = cw[t >> 2];
+      return (t & 3) == 0 ? q.x : (t & 3) == 1 ? q.y : (t & 3) == 2 ? q.z : q.w;
+    };
+    auto lookup = [&](uint32_t P, uint32_t (&e)[4]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t addr = perm(P, tsel, 0x0C0C0400u | ((4u + i) << 8));
+        // The table starts at LDS address 0: this kernel declares no static LDS.
+        e[i] = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(static_cast<uintptr_t>(addr));
+      }
+    };
+    uint32_t ebuf[kSgAhead + 1][4];
+#pragma unroll
+    for (int t = 0; t < kSgAhead; ++t) lookup(word(t), ebuf[t]);
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) {
+      f32x16 p = f32x16{};
+      if (kSgSpread && more) {  // this block's share of the next unit's DMA instructions
+#pragma unroll
+        for (int j = b * L::kCodeInstrs / BPW; j < (b + 1) * L::kCodeInstrs / BPW; ++j)
+          issue_part(j, u + 1, d_nxt, row_nxt);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int t = 4 * b + s;
+        if (t + kSgAhead < 4 * BPW) lookup(word(t + kSgAhead), ebuf[(t + kSgAhead) % (kSgAhead + 1)]);
+        // Keep those reads ahead of this sub-step's MFMAs (the scheduler would sink them to their use).
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t(&e)[4] = ebuf[t % (kSgAhead + 1)];
+        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[b][s], __builtin_bit_cast(f16x8, make_uint4(e[0], e[1], e[2], e[3])),
+                                                   p, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += p[r] * a[b];
+    }
+    wait_vmcnt<0>();  // this wave's DMAs of unit u+1 have landed
+    __syncthreads();  // ... everyone's, and every wave has summed unit u-1 from `red`
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    if (u + 1 < u_end) read_stage(u + 1);  // its latency overlaps the barrier
+    __syncthreads();
+    d_prev = d_cur;
+    row_prev = row_cur;
+    bias_prev = bias_cur;
+    g_cur = g_nxt;
+    d_cur = d_nxt;
+    row_cur = row_nxt;
   }
+  finish(0, d_prev, row_prev, bias_prev);
+  finish(1, d_prev, row_prev, bias_prev);
 }
 
 int cu_count() {
@@ -349,22 +575,35 @@ int cu_count() {
   return n;
 }
 
-// total_n: sum of the weights' row counts (an upper bound on the work, for the grid size).
-int launch_gemv_persistent(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const GemvDesc *descs, int count,
-                           const GemvDesc &one, int64_t total_n, const Code16 &c, hipStream_t s) {
-  const int64_t units = cdiv(total_n, kPgRows) + count;
-  const int64_t wgs_max = cu_count();
-  const int64_t grid = min(units, wgs_max);
-  const size_t lds = (kPgTableWords + kPgRedWords + count + 1) * sizeof(uint32_t);
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_gemv_persistent),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     (kPgTableWords + kPgRedWords + kPgMaxDescs + 1) * 4);
+// True when the streaming kernel covers K.
+bool stream_k(int64_t K) { return K == 1024 || K == 2048 || K == 3072; }
+
+template <int BPW>
+int launch_stream(const uint16_t *x, int64_t ldx, int64_t M, const GemvDesc *descs, int count, const GemvDesc &one,
+                  int64_t total_n, const Code16 &c, hipStream_t s) {
+  using L = SgLayout<BPW>;
+  const int64_t units = cdiv(total_n, kSgRows) + count;
+  const int64_t grid = min(units, static_cast<int64_t>(cu_count()));
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_gemv_stream<BPW>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, L::kMaxBytes);
   if (attr != hipSuccess)
-    return set_error(SELAS_EHIP, "nf4_linear: cannot reserve %d bytes of LDS: %s",
-                     (kPgTableWords + kPgRedWords + kPgMaxDescs + 1) * 4, hipGetErrorString(attr));
-  nf4_gemv_persistent<<<dim3(static_cast<uint32_t>(grid)), dim3(kPgThreads), lds, s>>>(
-      x, ldx, static_cast<int>(M), static_cast<int>(K), descs, count, one, c);
-  return check_launch("nf4_linear (persistent gemv)");
+    return set_error(SELAS_EHIP, "nf4_linear: cannot reserve %d bytes of LDS: %s", L::kMaxBytes,
+                     hipGetErrorString(attr));
+  const size_t lds = L::kPrefix + (count + 1) * sizeof(int);
+  nf4_gemv_stream<BPW><<<dim3(static_cast<uint32_t>(grid)), dim3(kSgThreads), lds, s>>>(
+      x, ldx, static_cast<int>(M), descs, count, one, c);
+  return check_launch("nf4_linear (streaming skinny gemm)");
+}
+
+// total_n: sum of the weights' row counts (an upper bound on the work, for the grid size).
+int launch_gemv_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const GemvDesc *descs, int count,
+                       const GemvDesc &one, int64_t total_n, const Code16 &c, hipStream_t s) {
+  switch (K) {
+    case 1024: return launch_stream<2>(x, ldx, M, descs, count, one, total_n, c, s);
+    case 2048: return launch_stream<4>(x, ldx, M, descs, count, one, total_n, c, s);
+    case 3072: return launch_stream<6>(x, ldx, M, descs, count, one, total_n, c, s);
+    default: return set_error(SELAS_EUNSUPPORTED, "nf4_linear: streaming skinny kernel takes K = 1024, 2048, 3072");
+  }
 }
 
 // =========================================================================== GEMM (M > 32)
@@ -427,13 +666,6 @@ __device__ __forceinline__ bf16x8 dequant8(const Tables &t, uint32_t P) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// s_waitcnt with only the vector-memory counter limited to N (gfx9 encoding:
-// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // LDS reads done, then a workgroup barrier; a compiler fence for LDS accesses.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -703,9 +935,9 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
   const uint16_t *xb = static_cast<const uint16_t *>(x);
   const uint16_t *bb = static_cast<const uint16_t *>(bias);
   uint16_t *yb = static_cast<uint16_t *>(y);
-  if (M <= 32 && K <= kPgWaves * kPgMaxKb * 64) {
+  if (M <= 32 && stream_k(K)) {
     const GemvDesc one{packed, absmax, bb, yb, N, ldy};
-    return launch_gemv_persistent(xb, ldx, M, K, nullptr, 1, one, N, c, s);
+    return launch_gemv_stream(xb, ldx, M, K, nullptr, 1, one, N, c, s);
   }
   if (M <= 32) {
     const int64_t grid = cdiv(N, 32 * kGemvGroups);
@@ -729,17 +961,19 @@ extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int
   if (!x || !descs || !code) return set_error(SELAS_EINVAL, "nf4_linear_grouped: null pointer");
   if (ldx < K) return set_error(SELAS_EINVAL, "nf4_linear_grouped: ldx below K");
   if (dtype != SELAS_BF16) return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: takes bf16");
-  if (blocksize != 64 || K % 64 || M > 32 || K > kPgWaves * kPgMaxKb * 64 || count > kPgMaxDescs)
-    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: needs blocksize 64, K %% 64 == 0, K <= %d, M <= 32, "
-                                         "at most %d weights", kPgWaves * kPgMaxKb * 64, kPgMaxDescs);
+  if (blocksize != 64 || !stream_k(K) || M > 32 || count > kSgMaxDescs)
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: needs blocksize 64, K = 1024, 2048 or 3072, M <= 32, "
+                                         "at most %d weights", kSgMaxDescs);
   if (!aligned(x, 16) || ldx % 8 || !aligned(descs, 8))
     return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: x rows must be 16-byte aligned");
   if (total_n <= 0 || total_n >= (1ll << 36))
     return set_error(SELAS_EINVAL, "nf4_linear_grouped: total_n must be the sum of the weights' row counts");
+  if (total_n * (K / 2) >= (1ll << 32))
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: a weight above 4 GiB");
   Code16 c;
   for (int i = 0; i < 16; ++i) c.v[i] = code[i];
   const GemvDesc none{nullptr, nullptr, nullptr, nullptr, 0, 0};
-  return launch_gemv_persistent(static_cast<const uint16_t *>(x), ldx, M, K,
+  return launch_gemv_stream(static_cast<const uint16_t *>(x), ldx, M, K,
                                 reinterpret_cast<const GemvDesc *>(descs), static_cast<int>(count), none,
                                 total_n, c, static_cast<hipStream_t>(stream));
 }

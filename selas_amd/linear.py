@@ -59,7 +59,7 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
         return F.linear(x, w, bias)
 
 
-GROUPED_MAX_K = 3072  # the grouped skinny kernel keeps x in registers: K <= 8 waves x 6 blocks x 64
+GROUPED_K = (1024, 2048, 3072)  # the grouped kernel keeps x in registers: K = 8 waves x 2, 4 or 6 blocks of 64
 GROUPED_MAX_M = 32
 
 
@@ -79,9 +79,10 @@ def nf4_linear_grouped(x: torch.Tensor, weights, code=None) -> list[torch.Tensor
     dev = _lib.require_gpu(x, *(w[0] for w in weights))
     x2 = _rows(x)
     m = x2.shape[0]
-    ok = (x.dtype == torch.bfloat16 and m <= GROUPED_MAX_M and k % 64 == 0 and k <= GROUPED_MAX_K
+    ok = (x.dtype == torch.bfloat16 and m <= GROUPED_MAX_M and k in GROUPED_K
           and x2.data_ptr() % 16 == 0 and x2.stride(0) % 8 == 0
-          and all(int(w[2]) == 64 and len(w[4]) == 2 and int(w[4][1]) == k for w in weights))
+          and all(int(w[2]) == 64 and len(w[4]) == 2 and int(w[4][1]) == k and w[0].data_ptr() % 16 == 0
+                  and w[1].data_ptr() % 4 == 0 for w in weights))
     if not ok:
         return [nf4_linear(x, *w) for w in weights]
     codes = {tuple(float(c) for c in w[3]) for w in weights}

@@ -77,8 +77,9 @@ def test_tiled_operand_is_the_reference_decode_bit_for_bit(dev):
     assert torch.equal(y, w_ref[:, ks].t())
 
 
-def test_skinny_operand_within_one_rounding(dev):
-    n, k, m = 192, 256, 16
+@pytest.mark.parametrize("n,k", [(192, 256), (96, 3072), (64, 1024)])
+def test_skinny_operand_within_one_rounding(dev, n, k):
+    m = 16
     p, a, w_ref = make_weight(n, k, 9, dev)
     ks = torch.randint(0, k, (m,), generator=seeded(10))
     x = torch.zeros(m, k, dtype=torch.bfloat16)
@@ -86,6 +87,26 @@ def test_skinny_operand_within_one_rounding(dev):
     y = nf4_linear(x.to(dev), p, a, 64, codecs.NF4_CODE, (n, k)).float().cpu()
     ref = w_ref[:, ks].t()
     assert ((y - ref).abs() <= 2.0 ** -7 * ref.abs()).all()
+
+
+def test_skinny_rows_of_any_magnitude(dev):
+    # The streaming skinny kernel rescales each row of x by a power of two before
+    # its fp16 products: rows far from 1, an all-zero row and a row with one huge
+    # entry must each match the oracle relative to that row alone.
+    n, k = 256, 3072
+    p, a, w_ref = make_weight(n, k, 31, dev)
+    b = (torch.randn(n, generator=seeded(33)) * 0.02).to(torch.bfloat16)
+    x = torch.randn(6, k, generator=seeded(32))
+    x[0] *= 2.0 ** -60
+    x[1] *= 2.0 ** 60
+    x[2] = 0.0
+    x[3, 17] = 3.0e38
+    x[4] = x[4].abs() + 1.0  # all positive: coherent sums
+    x = x.to(torch.bfloat16)
+    y = nf4_linear(x.to(dev), p, a, 64, codecs.NF4_CODE, (n, k), b.to(dev))
+    ref = oracle_linear(x, w_ref, b)
+    for r in range(6):
+        check_close(y[r:r + 1], ref[r:r + 1])
 
 
 def test_strided_and_batched_inputs(dev):

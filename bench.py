@@ -190,7 +190,7 @@ def bench_modulations(dev, steps, warmup):
     76 distinct weights (1.8 GB of NF4, beyond the 256 MB Infinity Cache): one grouped launch, and one launch
     per linear."""
     from selas_amd import codecs
-    from selas_amd.linear import nf4_linear_grouped
+    from selas_amd.linear import GroupedPlan, nf4_linear_grouped
 
     s = 28
     ws = [nf4_weight(6 * D, D, 400 + i, dev) for i in range(38)] + [nf4_weight(3 * D, D, 500 + i, dev) for i in range(38)]
@@ -208,22 +208,31 @@ def bench_modulations(dev, steps, warmup):
             if tm:
                 tm.stop(t)
 
+    plan = GroupedPlan(tuples, s, dev)
+    assert plan.supported
     for _ in range(warmup):
         run_each()
         nf4_linear_grouped(x, tuples)
+        plan.run(x)
     torch.cuda.synchronize(dev)
     tm = Timer()
     run_each(tm)
     for _ in range(max(3, steps // 2)):
-        t = tm.start("grouped")
+        t = tm.start("grouped_call")
         nf4_linear_grouped(x, tuples)
         tm.stop(t)
     torch.cuda.synchronize(dev)
+    for _ in range(max(5, steps)):
+        t = tm.start("grouped_kernel")
+        plan.run(x)
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
     per = tm.mean_ms("gemv")
-    grp = tm.mean_ms("grouped")
-    return {"launches": 76, "bytes": nbytes, "flops": flops, "grouped_ms": grp, "gbs_grouped": nbytes / grp / 1e6,
-            "frac_hbm_grouped": nbytes / grp / 1e6 / PEAK_HBM_GBS, "per_linear_kernel_ms_mean": per,
-            "gbs_per_linear": nbytes / (per * 76) / 1e6}
+    grp = tm.mean_ms("grouped_kernel")
+    call = tm.mean_ms("grouped_call")
+    return {"launches": 76, "bytes": nbytes, "flops": flops, "grouped_kernel_ms": grp,
+            "gbs_grouped": nbytes / grp / 1e6, "frac_hbm_grouped": nbytes / grp / 1e6 / PEAK_HBM_GBS,
+            "grouped_call_ms": call, "per_linear_kernel_ms_mean": per, "gbs_per_linear": nbytes / (per * 76) / 1e6}
 
 
 def bench_segments(dev, steps, warmup):
@@ -348,6 +357,35 @@ def cpu_baseline(target_s: float = 12.0):
                       f"extrapolated to 4608 rows: {step_s:.2f} s per step ({dec_s:.2f} s decode)"}
 
 
+# --------------------------------------------------------------------------- HBM traffic
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "nf4_gemm_block_linears_1024_traffic.md"
+
+
+def committed_traffic():
+    """HBM bytes per launch of the block-linear GEMM from the committed rocprofv3 --pmc summary (or None)."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(dev, gib: float = 1.0, reps: int = 3):
+    """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counter readings."""
+    n = int(gib * (1 << 30)) // 2
+    a = torch.empty(n, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize(dev)
+    log(f"bench: copy calibration {reps} x {n * 2} bytes")
+    del a, b
+
+
 # --------------------------------------------------------------------------- main
 
 
@@ -359,6 +397,8 @@ def main():
     ap.add_argument("--full-step", action="store_true", help="also time the full FLUX-dev-shaped step at 1024^2")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-calibration", action="store_true",
+                    help="first run a 1 GiB device copy (reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
@@ -366,6 +406,8 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     log(f"bench: {torch.cuda.get_device_name(dev)}")
+    if a.traffic_calibration:
+        copy_calibration(dev)
     res = bench_block_linears(dev, a.steps, a.warmup)
     log(f"bench: block linears {res['kernel_tflops']}")
     extra = {"block_linears": res}
@@ -401,7 +443,7 @@ def main():
                                "linear2 15360->3072, NF4 blocksize 64, bf16 activations", "tokens": M_1024,
                    "hidden": D, "mlp_hidden": MLP, "blocksize": 64, "weight_copies": 8},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None},
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": committed_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }

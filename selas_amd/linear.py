@@ -61,53 +61,86 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
 
 GROUPED_K = (1024, 2048, 3072)  # the grouped kernel keeps x in registers: K = 8 waves x 2, 4 or 6 blocks of 64
 GROUPED_MAX_M = 32
+GROUPED_MAX_WEIGHTS = 1023
 
 
-def nf4_linear_grouped(x: torch.Tensor, weights, code=None) -> list[torch.Tensor]:
+class GroupedPlan:
+    """A prepared grouped skinny launch: fixed NF4 weights, any x with ``rows`` rows.
+
+    ``weights``: sequence of (packed, absmax, blocksize, code, shape, bias) tuples sharing
+    K. The device descriptor table and the outputs are built once; ``run(x)`` is one
+    kernel launch and returns the plan's own output tensors, which the next ``run``
+    overwrites. ``supported`` is False when the grouped kernel does not cover the shapes
+    (then ``nf4_linear_grouped`` runs the linears one by one).
+    """
+
+    def __init__(self, weights, rows: int, device: torch.device, dtype: torch.dtype = torch.bfloat16):
+        self.weights = list(weights)
+        self.rows = int(rows)
+        self.k = int(self.weights[0][4][1]) if self.weights else 0
+        self.supported = bool(self.weights) and self._eligible(dtype)
+        self.outs: list[torch.Tensor] = []
+        self._keep: list[torch.Tensor] = []
+        self.desc = None
+        if not self.supported:
+            return
+        rows_tbl, total_n = [], 0
+        for packed, absmax, _, _, shape, bias in self.weights:
+            n = int(shape[0])
+            if bias is not None and (bias.dtype != dtype or not bias.is_contiguous()):
+                bias = bias.to(dtype).contiguous()
+                self._keep.append(bias)
+            y = torch.empty(self.rows, n, dtype=dtype, device=device)
+            self.outs.append(y)
+            rows_tbl.append([packed.data_ptr(), absmax.data_ptr(), 0 if bias is None else bias.data_ptr(),
+                             y.data_ptr(), n, n])
+            total_n += n
+        self.total_n = total_n
+        self.desc = torch.tensor(rows_tbl, dtype=torch.int64).to(device)
+        self.code = _lib.code_array(self.weights[0][3])
+
+    def _eligible(self, dtype) -> bool:
+        codes = {tuple(float(c) for c in w[3]) for w in self.weights}
+        return (dtype == torch.bfloat16 and 1 <= self.rows <= GROUPED_MAX_M and self.k in GROUPED_K
+                and len(codes) == 1 and len(self.weights) <= GROUPED_MAX_WEIGHTS
+                and all(int(w[2]) == 64 and len(w[4]) == 2 and int(w[4][1]) == self.k
+                        and w[0].data_ptr() % 16 == 0 and w[1].data_ptr() % 4 == 0 for w in self.weights))
+
+    def run(self, x: torch.Tensor) -> list[torch.Tensor]:
+        """Launch for x [rows, K] (bf16, unit column stride); returns the outputs [rows, n_i]."""
+        x2 = _rows(x)
+        if x2.shape != (self.rows, self.k) or x2.dtype != torch.bfloat16:
+            raise ValueError(f"plan expects x [{self.rows}, {self.k}] bf16, got {tuple(x2.shape)} {x2.dtype}")
+        if x2.data_ptr() % 16 or x2.stride(0) % 8:
+            raise ValueError("x rows must be 16-byte aligned")
+        dev = _lib.require_gpu(x2, self.desc)
+        with torch.cuda.device(dev):
+            _lib.call("selas_nf4_linear_grouped", x2.data_ptr(), self.rows, self.k, x2.stride(0), self.desc.data_ptr(),
+                      len(self.weights), self.total_n, 64, self.code, _lib.BF16, _lib.stream(dev))
+        return self.outs
+
+
+def nf4_linear_grouped(x: torch.Tensor, weights) -> list[torch.Tensor]:
     """``[F.linear(x, decode(W_i), b_i) for W_i, b_i in weights]`` in one launch.
 
     ``weights``: sequence of (packed, absmax, blocksize, code, shape, bias) tuples that
-    share ``x`` [..., K] with at most 32 rows. Each result has the bits ``nf4_linear``
-    gives for that weight alone. This is the hoisted modulation prologue
-    (selas/models/flux.py:428-445): every modulation linear of a model applied to
-    one silu(vec). Shapes the grouped kernel does not cover are run one by one.
+    share ``x`` [..., K] with at most 32 rows. Each result is a new tensor with the bits
+    ``nf4_linear`` gives for that weight alone. This is the hoisted modulation prologue
+    (selas/models/flux.py:428-445): every modulation linear of a model applied to one
+    silu(vec). Shapes the grouped kernel does not cover are run one by one.
     """
     weights = list(weights)
     if not weights:
         return []
-    k = x.shape[-1]
     dev = _lib.require_gpu(x, *(w[0] for w in weights))
     x2 = _rows(x)
-    m = x2.shape[0]
-    ok = (x.dtype == torch.bfloat16 and m <= GROUPED_MAX_M and k in GROUPED_K
-          and x2.data_ptr() % 16 == 0 and x2.stride(0) % 8 == 0
-          and all(int(w[2]) == 64 and len(w[4]) == 2 and int(w[4][1]) == k and w[0].data_ptr() % 16 == 0
-                  and w[1].data_ptr() % 4 == 0 for w in weights))
-    if not ok:
+    plan = GroupedPlan(weights, x2.shape[0], dev, x.dtype)
+    if not plan.supported or x2.data_ptr() % 16 or x2.stride(0) % 8 or x2.shape[1] != plan.k:
         return [nf4_linear(x, *w) for w in weights]
-    codes = {tuple(float(c) for c in w[3]) for w in weights}
-    if len(codes) != 1:
-        return [nf4_linear(x, *w) for w in weights]
-    outs, rows, total_n = [], [], 0
-    converted = []  # converted biases stay referenced until the launch is queued
-    for packed, absmax, _, _, shape, bias in weights:
-        n = int(shape[0])
-        if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
-            bias = bias.to(x.dtype).contiguous()
-            converted.append(bias)
-        y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
-        outs.append(y)
-        rows.append([packed.data_ptr(), absmax.data_ptr(), 0 if bias is None else bias.data_ptr(), y.data_ptr(),
-                     n, n])
-        total_n += n
-    desc = torch.tensor(rows, dtype=torch.int64).to(dev, non_blocking=False)
-    with torch.cuda.device(dev):
-        _lib.call("selas_nf4_linear_grouped", x2.data_ptr(), m, k, x2.stride(0), desc.data_ptr(), len(weights), total_n,
-                  64, _lib.code_array(next(iter(codes))), _lib.BF16, _lib.stream(dev))
-    # desc and converted biases may be freed now: the caching allocator hands their memory only to
-    # later work on this same stream, which runs after the launch.
-    del converted
-    return outs
+    outs = plan.run(x2)
+    # The plan's descriptor table may be freed now: the caching allocator hands its memory
+    # only to later work on this same stream, which runs after the launch.
+    return [y.view(*x.shape[:-1], y.shape[-1]) for y in outs]
 
 
 class UnitView:

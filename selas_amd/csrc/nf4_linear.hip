@@ -776,6 +776,26 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < MB; ++j) load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
   };
+  // The same loads in four parts, one per sub-step, so that a wave never
+  // queues a whole block's loads at once (issue would stall on the address
+  // unit instead of overlapping the MFMAs): part 0 the codes, scales and the
+  // first x loads, parts 1-3 the rest of the x tile.
+  constexpr int XPP = MB / 4;                 // x loads per part
+  constexpr int P3 = XPP;                     // loads in part 3
+  auto issue_part = [&](int stage, int blk, int part, uint4 (&bq)[CB], float (&bs)[CB]) {
+    const uint32_t kb = static_cast<uint32_t>(blk);
+    if (part == 0) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        bq[cb] = load_b128(wr, b_voff[cb], kb * 32u);
+        bs[cb] = load_f32(sr, s_voff[cb], kb * 4u);
+      }
+    }
+    uint8_t *dst = a_dst + stage * SB;
+#pragma unroll
+    for (int j = XPP * part; j < XPP * (part + 1); ++j)
+      load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
+  };
   auto frag = [&](int kb, int s, int mb) {
     return *reinterpret_cast<const bf16x8 *>(smem + (kb % STAGES) * SB + a_rd[s] + mb * 4096);
   };
@@ -817,16 +837,29 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
   // name, never by copying registers that a load in flight still targets.
   auto block = [&](int kb, const uint4 (&cq)[CB], const uint4 (&nq)[CB], const float (&ns)[CB], uint4 (&fq)[CB],
                    float (&fs)[CB]) {
-    issue((kb + LOOK) % STAGES, min(kb + LOOK, kblocks - 1), fq, fs);
+    const int fstage = (kb + LOOK) % STAGES, fblk = min(kb + LOOK, kblocks - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
       if (s < 3) {
+        if constexpr (LOOK >= 2) {
+          issue_part(fstage, fblk, s, fq, fs);
+        } else if (s == 0) {
+#pragma unroll
+          for (int part = 0; part < 4; ++part) issue_part(fstage, fblk, part, fq, fs);
+        }
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) wf[nxt][cb] = dequant8(tab[cb], word(cq[cb], s + 1));
       } else {
-        wait_vmcnt<(LOOK - 1) * LPB>();
-        lds_barrier();
+        if constexpr (LOOK >= 2) {
+          // Block kb+1's loads are older than parts 0-2 of block kb+LOOK's.
+          wait_vmcnt<(LOOK - 1) * LPB - P3>();
+          lds_barrier();
+          issue_part(fstage, fblk, 3, fq, fs);
+        } else {
+          wait_vmcnt<0>();
+          lds_barrier();
+        }
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
           tab[cb] = make_tables(cl, ns[cb]);

@@ -897,22 +897,72 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
   (void)bs2;
 
   // Epilogue: acc[mb][cb] holds D[n][m] for n = n0 + WN*wave + 32*cb + 8*(r/4) + 4*h + r%4
-  // and m = m0 + 32*mb + c; four consecutive n per r/4 are stored as one 8-byte write.
+  // and m = m0 + 32*mb + c. Bias is added in fp32 and the sum rounded once.
+  float bv[CB][4][4];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h + t4;
+        bv[cb][q][t4] = (bias && n < N) ? bf16_bits_to_f32(bias[n]) : 0.0f;
+      }
+  const bool full_cols = n0 + WN * (wave + 1) <= N;
+  if (full_cols && (ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+    // Through LDS, so that every store writes whole 128-byte row segments: a
+    // direct store from the MFMA layout writes 16 bytes into each of 32 rows,
+    // and each partial line then reaches HBM as a write of its own. Each wave
+    // stages 32*MB/2 rows x WN columns at a time (row stride WN*2+8 bytes: the
+    // 8-byte writes of 32 lanes then hit distinct banks).
+    constexpr int RS = WN * 2 + 8, HALF = MB / 2;
+    static_assert(4 * HALF * 32 * RS <= STAGES * SB, "epilogue staging fits the x stages");
+    __syncthreads();  // every wave is done with the x stages
+    uint8_t *ep = smem + wave * HALF * 32 * RS;
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(Y, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldy * 2,
+                                                                             static_cast<int64_t>(0xffffffff))));
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int mh = 0; mh < HALF; ++mh) {
+        const int mb = HALF * half + mh;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = pack_bf16x2(acc[mb][cb][4 * q] + bv[cb][q][0], acc[mb][cb][4 * q + 1] + bv[cb][q][1]);
+            const uint32_t hi = pack_bf16x2(acc[mb][cb][4 * q + 2] + bv[cb][q][2], acc[mb][cb][4 * q + 3] + bv[cb][q][3]);
+            *reinterpret_cast<uint2 *>(ep + (32 * mh + c) * RS + 2 * (32 * cb + 8 * q + 4 * h)) = make_uint2(lo, hi);
+          }
+      }
+      // Row r of the staged block: 8 lanes x 16 bytes; a wave stores 8 rows per instruction.
+#pragma unroll
+      for (int j = 0; j < HALF * 4; ++j) {
+        const int r = 8 * j + (lane >> 3), col = 8 * (lane & 7);
+        const uint8_t *src = ep + r * RS + 2 * col;
+        const uint2 v0 = *reinterpret_cast<const uint2 *>(src), v1 = *reinterpret_cast<const uint2 *>(src + 8);
+        const int m = m0 + 32 * HALF * half + r;
+        // Rows past M fall outside the buffer range and are dropped.
+        const uint32_t off = m < M ? static_cast<uint32_t>((static_cast<int64_t>(m) * ldy + n0 + WN * wave + col) * 2)
+                                   : 0xffffffffu;
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v0.x, v0.y, v1.x, v1.y}, yr, off, 0, 0);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h;
-      float bv[4];
-#pragma unroll
-      for (int t4 = 0; t4 < 4; ++t4) bv[t4] = (bias && n + t4 < N) ? bf16_bits_to_f32(bias[n + t4]) : 0.0f;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const int m = m0 + 32 * mb + c;
         if (m >= M) continue;
         uint16_t *dst = Y + static_cast<int64_t>(m) * ldy + n;
-        const float v0 = acc[mb][cb][4 * q] + bv[0], v1 = acc[mb][cb][4 * q + 1] + bv[1];
-        const float v2 = acc[mb][cb][4 * q + 2] + bv[2], v3 = acc[mb][cb][4 * q + 3] + bv[3];
+        const float v0 = acc[mb][cb][4 * q] + bv[cb][q][0], v1 = acc[mb][cb][4 * q + 1] + bv[cb][q][1];
+        const float v2 = acc[mb][cb][4 * q + 2] + bv[cb][q][2], v3 = acc[mb][cb][4 * q + 3] + bv[cb][q][3];
         if (n + 3 < N) {
           *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
         } else {

@@ -8,9 +8,11 @@
 // Row kernels (LayerNorm-based) use one 256-thread workgroup per token row:
 // the row stays in registers between the mean pass, the variance pass and the
 // output pass (two-pass statistics in fp32), and the cross-wave sums are
-// combined in a fixed order. Attention prep uses one wavefront per (token,
-// head): lane i owns the interleaved RoPE pair (2i, 2i+1), so the RMS sum is
-// one wave reduction and the rotation needs no data exchange.
+// combined in a fixed order. Attention prep gives each thread 8 consecutive
+// channels of q, k and v (16-byte accesses); the Dh/8 threads of a head are
+// adjacent lanes, so the RMS sum is a short cross-lane reduction and the
+// interleaved RoPE pairs stay in-thread (other head sizes and alignments: one
+// wavefront per (token, head), lane i owning the pair (2i, 2i+1)).
 #include "common.h"
 
 namespace selas {
@@ -22,14 +24,13 @@ constexpr float kFp16Max = 65504.0f;
 constexpr float kLnEps = 1e-6f;
 constexpr float kRmsEps = 1e-6f;
 
-// Sum over the 256 threads of a workgroup, combined in wave order.
-__device__ __forceinline__ float block_sum(float v, float *scratch) {
+// Sum over the 256 threads of a workgroup, combined in wave order. Each call
+// site passes its own 4-float slot, so one barrier suffices.
+__device__ __forceinline__ float block_sum(float v, float *slot) {
   v = wave_sum(v);
-  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = v;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
-  __syncthreads();
-  return ((scratch[0] + scratch[1]) + scratch[2]) + scratch[3];
+  return ((slot[0] + slot[1]) + slot[2]) + slot[3];
 }
 
 __device__ __forceinline__ float clamp_guard(float v) {
@@ -83,7 +84,7 @@ __device__ __forceinline__ void ln_modulate_store(float4 (&v)[kMaxVec], int nvec
       const float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
       q += (a * a + b * b) + (c * c + d * d);
     }
-  const float var = block_sum(q, scratch) / static_cast<float>(D);
+  const float var = block_sum(q, scratch + 4) / static_cast<float>(D);
   const float rstd = 1.0f / sqrtf(var + kLnEps);
 #pragma unroll
   for (int j = 0; j < kMaxVec; ++j) {
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kRowThreads) void mod_in_kernel(const float *__rest
                                                              int64_t x_sl, const float *__restrict__ shift,
                                                              const float *__restrict__ scale, int64_t mod_sb,
                                                              void *__restrict__ out) {
-  __shared__ float scratch[4];
+  __shared__ float scratch[8];  // two block sums
   const int row = blockIdx.x;
   const int b = row / L, l = row - b * L;
   const float *xr = x + b * x_sb + l * x_sl;
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kRowThreads) void gated_add_kernel(
     const float *__restrict__ x, int L, int D, int64_t x_sb, int64_t x_sl, const float *__restrict__ g, int64_t g_sb,
     const void *__restrict__ y, int64_t y_sb, int64_t y_sl, int guard, const float *__restrict__ shift,
     const float *__restrict__ scale, int64_t mod_sb, float *__restrict__ x_out, void *__restrict__ h) {
-  __shared__ float scratch[4];
+  __shared__ float scratch[8];  // two block sums
   const int row = blockIdx.x;
   const int b = row / L, l = row - b * L;
   const float *xr = x + b * x_sb + l * x_sl;
@@ -233,6 +234,78 @@ __global__ __launch_bounds__(256) void qkv_prep_kernel(HeadSrc s0, HeadSrc s1, i
   (void)xv;
 }
 
+// Attention prep, 8 channels per thread. Thread t of a (batch, joint row)
+// takes channels [8*(t % LPH), +8) of head t / LPH (LPH = Dh / 8 adjacent
+// lanes per head, so a head never straddles a wave); rows follow each other
+// in thread order, so every access is a 16-byte vector.
+template <int DT, int LPH>
+__global__ __launch_bounds__(256) void qkv_prep_vec_kernel(HeadSrc s0, HeadSrc s1, int B, int H,
+                                                           const float *__restrict__ cos,
+                                                           const float *__restrict__ sin, uint16_t *__restrict__ q,
+                                                           uint16_t *__restrict__ k, uint16_t *__restrict__ v) {
+  constexpr int Dh = 8 * LPH, half = Dh / 2;
+  const int Lj = s0.L + s1.L, per_row = H * LPH, HD = H * Dh;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const bool live = item < static_cast<int64_t>(B) * Lj * per_row;
+  const int64_t bl = live ? item / per_row : 0;
+  const int t = static_cast<int>(item - bl * per_row);
+  const int hh = live ? t / LPH : 0, part = t % LPH;
+  const int l = static_cast<int>(bl % Lj), b = static_cast<int>(bl / Lj);
+  const bool first = l < s0.L;
+  const HeadSrc &s = first ? s0 : s1;
+  const int ls = first ? l : l - s0.L;
+  const int d0 = 8 * part;
+  float xq[8] = {}, xk[8] = {}, cs[4] = {1, 1, 1, 1}, sn[4] = {}, qs[8] = {}, ks[8] = {};
+  uint4 vv = make_uint4(0, 0, 0, 0);
+  if (live) {
+    const uint16_t *base = s.qkv + b * s.sb + ls * s.sl + hh * Dh + d0;
+    const uint4 uq = *reinterpret_cast<const uint4 *>(base), uk = *reinterpret_cast<const uint4 *>(base + HD);
+    vv = *reinterpret_cast<const uint4 *>(base + 2 * HD);
+    const uint32_t wq[4] = {uq.x, uq.y, uq.z, uq.w}, wk[4] = {uk.x, uk.y, uk.z, uk.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 a = load_pair<DT>(reinterpret_cast<const uint16_t *>(&wq[i]));
+      const float2 c = load_pair<DT>(reinterpret_cast<const uint16_t *>(&wk[i]));
+      xq[2 * i] = a.x; xq[2 * i + 1] = a.y; xk[2 * i] = c.x; xk[2 * i + 1] = c.y;
+    }
+    const float4 c4 = *reinterpret_cast<const float4 *>(cos + static_cast<int64_t>(l) * half + 4 * part);
+    const float4 s4 = *reinterpret_cast<const float4 *>(sin + static_cast<int64_t>(l) * half + 4 * part);
+    cs[0] = c4.x; cs[1] = c4.y; cs[2] = c4.z; cs[3] = c4.w;
+    sn[0] = s4.x; sn[1] = s4.y; sn[2] = s4.z; sn[3] = s4.w;
+    const float4 q0 = *reinterpret_cast<const float4 *>(s.qs + d0), q1 = *reinterpret_cast<const float4 *>(s.qs + d0 + 4);
+    const float4 k0 = *reinterpret_cast<const float4 *>(s.ks + d0), k1 = *reinterpret_cast<const float4 *>(s.ks + d0 + 4);
+    qs[0] = q0.x; qs[1] = q0.y; qs[2] = q0.z; qs[3] = q0.w; qs[4] = q1.x; qs[5] = q1.y; qs[6] = q1.z; qs[7] = q1.w;
+    ks[0] = k0.x; ks[1] = k0.y; ks[2] = k0.z; ks[3] = k0.w; ks[4] = k1.x; ks[5] = k1.y; ks[6] = k1.z; ks[7] = k1.w;
+  }
+  // RMS over the head: this thread's 8 squares, then the LPH adjacent lanes (every lane takes part).
+  float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    sq += xq[i] * xq[i];
+    sk += xk[i] * xk[i];
+  }
+#pragma unroll
+  for (int o = 1; o < LPH; o <<= 1) {
+    sq += __shfl_xor(sq, o, 64);
+    sk += __shfl_xor(sk, o, 64);
+  }
+  if (!live) return;
+  const float rq = 1.0f / sqrtf(sq / static_cast<float>(Dh) + kRmsEps);
+  const float rk = 1.0f / sqrtf(sk / static_cast<float>(Dh) + kRmsEps);
+  uint32_t oq[4], ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = (xq[2 * i] * rq) * qs[2 * i], bq = (xq[2 * i + 1] * rq) * qs[2 * i + 1];
+    oq[i] = pack_pair<DT>(a * cs[i] - bq * sn[i], a * sn[i] + bq * cs[i]);
+    const float c = (xk[2 * i] * rk) * ks[2 * i], bk = (xk[2 * i + 1] * rk) * ks[2 * i + 1];
+    ok[i] = pack_pair<DT>(c * cs[i] - bk * sn[i], c * sn[i] + bk * cs[i]);
+  }
+  const int64_t o = ((static_cast<int64_t>(b) * H + hh) * Lj + l) * Dh + d0;
+  *reinterpret_cast<uint4 *>(q + o) = make_uint4(oq[0], oq[1], oq[2], oq[3]);
+  *reinterpret_cast<uint4 *>(k + o) = make_uint4(ok[0], ok[1], ok[2], ok[3]);
+  *reinterpret_cast<uint4 *>(v + o) = vv;
+}
+
 // ------------------------------------------------------------------ GELU / concat
 
 __device__ __forceinline__ float gelu_tanh(float x) {
@@ -240,6 +313,16 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float kKappa = 0.044715f;
   const float inner = kBeta * (x + kKappa * x * x * x);
   return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// The same function through 0.5 * (1 + tanh(z)) = 1 / (1 + exp(-2z)): one
+// hardware exponential and one reciprocal instead of tanhf (a few ulp of fp32,
+// below the rounding to a 16-bit output).
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float kKappa = 0.044715f;
+  const float z = kBeta * (x + kKappa * x * x * x);
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * z));
 }
 
 // out[r, 0:Da] = a[r, :] and out[r, Da:Da+Dm] = gelu(m[r, :]); Da may be 0.
@@ -271,14 +354,14 @@ __global__ __launch_bounds__(256) void concat_gelu_kernel(const uint16_t *__rest
           float lo, hi;
           if constexpr (DT == SELAS_BF16) { lo = bf16_bits_to_f32(w[t] & 0xffffu); hi = bf16_bits_to_f32(w[t] >> 16); }
           else { lo = f16_bits_to_f32(w[t] & 0xffffu); hi = f16_bits_to_f32(w[t] >> 16); }
-          o[t] = pack_pair<DT>(gelu_tanh(lo), gelu_tanh(hi));
+          o[t] = pack_pair<DT>(gelu_tanh_fast(lo), gelu_tanh_fast(hi));
         }
         *reinterpret_cast<uint4 *>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
       } else {
         float xv;
         if constexpr (DT == SELAS_BF16) xv = bf16_bits_to_f32(*src);
         else xv = f16_bits_to_f32(*src);
-        *dst = DT == SELAS_BF16 ? bf16_bits_rne(gelu_tanh(xv)) : f16_bits_rne(gelu_tanh(xv));
+        *dst = DT == SELAS_BF16 ? bf16_bits_rne(gelu_tanh_fast(xv)) : f16_bits_rne(gelu_tanh_fast(xv));
       }
     }
   }
@@ -411,8 +494,30 @@ int qkv_launch(const char *what, HeadSrc s0, HeadSrc s1, int64_t B, int64_t H, i
       return set_error(SELAS_EUNSUPPORTED, "%s: qkv rows must be 4-byte aligned", what);
   if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4)) return set_error(SELAS_EUNSUPPORTED, "%s: misaligned output", what);
   if (items / 4 >= (1ll << 31)) return set_error(SELAS_EUNSUPPORTED, "%s: too many rows", what);
-  const dim3 grid(static_cast<uint32_t>(cdiv(items, 4))), blk(256);
   uint16_t *qo = static_cast<uint16_t *>(q), *ko = static_cast<uint16_t *>(k), *vo = static_cast<uint16_t *>(v);
+  // 16-byte path: Dh in {16, 32, 64, 128}, every row and output 16-byte aligned.
+  bool vec = (Dh == 16 || Dh == 32 || Dh == 64 || Dh == 128) && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+             aligned(cos, 16) && aligned(sin, 16) && (H * Dh) % 8 == 0 && items * (Dh / 8) < (1ll << 31);
+  for (const HeadSrc *s : {&s0, &s1})
+    if (s->L > 0) vec = vec && aligned(s->qkv, 16) && s->sb % 8 == 0 && s->sl % 8 == 0 && aligned(s->qs, 16) &&
+                        aligned(s->ks, 16);
+  if (vec) {
+    const dim3 vgrid(static_cast<uint32_t>(cdiv(items * (Dh / 8), 256))), vblk(256);
+#define SELAS_QV(DT, LPH) \
+  qkv_prep_vec_kernel<DT, LPH><<<vgrid, vblk, 0, st>>>(s0, s1, (int)B, (int)H, cos, sin, qo, ko, vo)
+#define SELAS_QV_DT(DT)                   \
+  switch (Dh) {                           \
+    case 16: SELAS_QV(DT, 2); break;      \
+    case 32: SELAS_QV(DT, 4); break;      \
+    case 64: SELAS_QV(DT, 8); break;      \
+    default: SELAS_QV(DT, 16);            \
+  }
+    if (dtype == SELAS_BF16) { SELAS_QV_DT(SELAS_BF16) } else { SELAS_QV_DT(SELAS_F16) }
+#undef SELAS_QV_DT
+#undef SELAS_QV
+    return check_launch(what);
+  }
+  const dim3 grid(static_cast<uint32_t>(cdiv(items, 4))), blk(256);
   if (dtype == SELAS_BF16)
     qkv_prep_kernel<SELAS_BF16><<<grid, blk, 0, st>>>(s0, s1, (int)B, (int)H, (int)Dh, cos, sin, qo, ko, vo);
   else

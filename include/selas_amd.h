@@ -96,6 +96,37 @@ int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uin
                      const float *absmax, int64_t blocksize, const float code[16], int64_t N,
                      const void *bias, void *y, int64_t ldy, int dtype, void *stream);
 
+/* At most this many linears per selas_nf4_linear_batched call. */
+#define SELAS_MAX_BATCHED_LINEARS 4
+
+/* One quantized linear of a batched launch (host-memory array element); the
+ * fields mean what the arguments of selas_nf4_linear mean. */
+typedef struct selas_nf4_gemm_problem {
+  const void *x;
+  int64_t M, K, ldx;
+  const uint8_t *packed;
+  const float *absmax;
+  int64_t N;
+  const void *bias;
+  void *y;
+  int64_t ldy;
+} selas_nf4_gemm_problem;
+
+/*
+ * Up to SELAS_MAX_BATCHED_LINEARS independent quantized linears (each its own
+ * x, weight, bias and y; all M > 32) in one launch of the tiled GEMM: the
+ * tiles of all problems share the GPU, so a small problem fills the CUs a
+ * large one leaves idle in its last round. Each y has the bits
+ * selas_nf4_linear gives for that problem alone. Returns SELAS_EUNSUPPORTED,
+ * launching nothing, when any problem is outside the tiled GEMM (M <= 32 or
+ * any reason selas_nf4_linear would give); the caller then runs them one by one.
+ * No counterpart in the reference: it replaces consecutive UnitView.linear
+ * calls on independent inputs, e.g. the image and text streams of FLUX's
+ * double block (selas/models/flux.py:300-324).
+ */
+int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
+                             const float code[16], int dtype, void *stream);
+
 /*
  * One NF4 weight of a grouped skinny linear (device-memory array element).
  * packed/absmax as for selas_nf4_linear, bias [n] bf16 or NULL, y [M, n] bf16

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, list] = {
     "selas_nf4_encode": [_P, _I64, _I64, _F16x, _P, _P, _P],
     "selas_nf4_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _F16x, _I64, _P, _P, _I64, _INT, _P],
     "selas_nf4_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F16x, _INT, _P],
+    "selas_nf4_linear_batched": [_P, _I64, _I64, _F16x, _INT, _P],
     "selas_mod_in": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _INT, _P],
     "selas_gated_add": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P],
     "selas_gated_add_mod": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P, _I64,
@@ -39,6 +40,16 @@ SIGNATURES: dict[str, list] = {
     "selas_gelu": [_P, _I64, _I64, _I64, _P, _INT, _P],
     "selas_attn_mlp": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _INT, _P],
 }
+
+
+MAX_BATCHED_LINEARS = 4
+
+
+class GemmProblem(ctypes.Structure):
+    """selas_nf4_gemm_problem (include/selas_amd.h)."""
+
+    _fields_ = [("x", _P), ("M", _I64), ("K", _I64), ("ldx", _I64), ("packed", _P), ("absmax", _P), ("N", _I64),
+                ("bias", _P), ("y", _P), ("ldy", _I64)]
 
 
 class Unsupported(NotImplementedError):

@@ -707,23 +707,48 @@ __device__ __forceinline__ void interleave_substep() {
 //   * before sub-step 3 the block kb+1 loads are waited for and the
 //     workgroup synchronises; sub-step 3 then overlaps with building the
 //     product tables and first fragments of block kb+1.
+// One problem of a batched launch; its tiles are global tiles [tile0, tile0 + tiles_m * tiles_n).
+struct GemmProblem {
+  const uint16_t *X;
+  const uint8_t *packed;
+  const float *absmax;
+  const uint16_t *bias;
+  uint16_t *Y;
+  int64_t ldx, ldy;
+  int M, K, N, tiles_n, tile0;
+};
+constexpr int kGemmMaxProblems = 4;
+struct GemmBatch {
+  GemmProblem p[kGemmMaxProblems];
+  int count, tiles, per_xcd;
+};
+
 template <int MB, int CB, int STAGES>
-__global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
-    const uint16_t *__restrict__ X, int64_t ldx, int M, int K, const uint8_t *__restrict__ packed,
-    const float *__restrict__ absmax, Code16 code, int N, const uint16_t *__restrict__ bias,
-    uint16_t *__restrict__ Y, int64_t ldy, int tiles_n, int tiles, int per_xcd) {
+__global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
   constexpr int TM = 32 * MB, WN = 32 * CB, TN = 4 * WN;
   constexpr int SB = TM * 128;  // bytes of one x stage: TM rows x 64 bf16
   constexpr int LOOK = STAGES - 1;
   constexpr int LPB = 2 * CB + MB;  // vector-memory loads issued per K block and wave
   static_assert(MB * CB == 16 && (STAGES == 2 || STAGES == 3), "tile shape");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB];
-  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (t >= tiles) return;
+  const int t = (blockIdx.x & 7) * batch.per_xcd + (blockIdx.x >> 3);
+  if (t >= batch.tiles) return;
+  // The problem this tile belongs to (uniform: scalar selects over the kernel arguments).
+  GemmProblem P = batch.p[0];
+#pragma unroll
+  for (int i = 1; i < kGemmMaxProblems; ++i)
+    if (i < batch.count && t >= batch.p[i].tile0) P = batch.p[i];
+  const uint16_t *__restrict__ X = P.X;
+  const uint8_t *__restrict__ packed = P.packed;
+  const float *__restrict__ absmax = P.absmax;
+  const uint16_t *__restrict__ bias = P.bias;
+  uint16_t *__restrict__ Y = P.Y;
+  const int64_t ldx = P.ldx, ldy = P.ldy;
+  const int M = P.M, K = P.K, N = P.N, tiles_n = P.tiles_n;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c = lane & 31;
-  const int tm = t / tiles_n, tn = t - tm * tiles_n;
+  const int tm = (t - P.tile0) / tiles_n, tn = (t - P.tile0) - tm * tiles_n;
   const int m0 = tm * TM, n0 = tn * TN;
   const int kblocks = K >> 6;
   const uint32_t ldx_b = static_cast<uint32_t>(ldx) * 2u;
@@ -974,14 +999,20 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(
   }
 }
 
+// `batch.p[0..count)` filled except tiles_n / tile0, which are set here.
 template <int MB, int CB, int STAGES>
-void launch_gemm(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const uint8_t *packed, const float *absmax,
-                 const Code16 &c, int64_t N, const uint16_t *bias, uint16_t *y, int64_t ldy, hipStream_t s) {
-  const int64_t tiles_m = cdiv(M, 32 * MB), tiles_n = cdiv(N, 128 * CB), tiles = tiles_m * tiles_n;
-  const int64_t per_xcd = cdiv(tiles, 8);
-  nf4_gemm_kernel<MB, CB, STAGES><<<dim3(static_cast<uint32_t>(per_xcd * 8)), dim3(kGemmThreads), 0, s>>>(
-      x, ldx, static_cast<int>(M), static_cast<int>(K), packed, absmax, c, static_cast<int>(N), bias, y, ldy,
-      static_cast<int>(tiles_n), static_cast<int>(tiles), static_cast<int>(per_xcd));
+void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s) {
+  int64_t tiles = 0;
+  for (int i = 0; i < batch.count; ++i) {
+    GemmProblem &p = batch.p[i];
+    const int64_t tiles_m = cdiv(p.M, 32 * MB), tiles_n = cdiv(p.N, 128 * CB);
+    p.tiles_n = static_cast<int>(tiles_n);
+    p.tile0 = static_cast<int>(tiles);
+    tiles += tiles_m * tiles_n;
+  }
+  batch.tiles = static_cast<int>(tiles);
+  batch.per_xcd = static_cast<int>(cdiv(tiles, 8));
+  nf4_gemm_kernel<MB, CB, STAGES><<<dim3(static_cast<uint32_t>(batch.per_xcd * 8)), dim3(kGemmThreads), 0, s>>>(batch, c);
 }
 
 }  // namespace
@@ -989,29 +1020,44 @@ void launch_gemm(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const uin
 
 using namespace selas;
 
+namespace {
+// Validation shared by the single and batched entries: SELAS_OK when the fused
+// kernels take the call, or the error (EUNSUPPORTED: the caller falls back).
+int check_linear(const char *what, const void *x, int64_t M, int64_t K, int64_t ldx, const uint8_t *packed,
+                 const float *absmax, int64_t blocksize, const float *code, int64_t N, const void *bias,
+                 const void *y, int64_t ldy, int dtype) {
+  if (M < 0 || K <= 0 || N <= 0)
+    return set_error(SELAS_EINVAL, "%s: bad shape M=%lld K=%lld N=%lld", what, (long long)M, (long long)K,
+                     (long long)N);
+  if (!valid_dtype(dtype)) return set_error(SELAS_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (ldx < K || ldy < N)
+    return set_error(SELAS_EINVAL, "%s: row strides ldx=%lld ldy=%lld below K, N", what, (long long)ldx,
+                     (long long)ldy);
+  if (M == 0) return SELAS_OK;
+  if (!x || !packed || !absmax || !y || !code) return set_error(SELAS_EINVAL, "%s: null pointer", what);
+  if (dtype != SELAS_BF16)
+    return set_error(SELAS_EUNSUPPORTED, "%s: fused kernels take bf16, got %s", what, dtype_name(dtype));
+  if (blocksize != 64 || K % 64)
+    return set_error(SELAS_EUNSUPPORTED, "%s: fused kernels need blocksize 64 and K %% 64 == 0 (blocksize %lld, K %lld)",
+                     what, (long long)blocksize, (long long)K);
+  if (!aligned(x, 16) || ldx % 8 || !aligned(packed, 16) || !aligned(absmax, 4) || !aligned(y, 8) || ldy % 4 ||
+      (bias && !aligned(bias, 2)))
+    return set_error(SELAS_EUNSUPPORTED, "%s: fused kernels need 16-byte aligned x rows and codes, "
+                                         "8-byte aligned y rows", what);
+  // Buffer offsets are 32-bit: every operand (plus one tile of overhang) must span < 4 GiB.
+  const int64_t lim = (1ll << 32) - 1;
+  if ((M + 512) * ldx * 2 > lim || (N + 256) * (K / 2) > lim || (N + 256) * (K / 64) * 4 > lim || M * ldy * 2 > lim)
+    return set_error(SELAS_EUNSUPPORTED, "%s: operand above 4 GiB", what);
+  return SELAS_OK;
+}
+}  // namespace
+
 extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uint8_t *packed,
                                 const float *absmax, int64_t blocksize, const float code[16], int64_t N,
                                 const void *bias, void *y, int64_t ldy, int dtype, void *stream) {
-  if (M < 0 || K <= 0 || N <= 0) return set_error(SELAS_EINVAL, "nf4_linear: bad shape M=%lld K=%lld N=%lld",
-                                                   (long long)M, (long long)K, (long long)N);
-  if (!valid_dtype(dtype)) return set_error(SELAS_EINVAL, "nf4_linear: bad dtype %d", dtype);
-  if (ldx < K || ldy < N) return set_error(SELAS_EINVAL, "nf4_linear: row strides ldx=%lld ldy=%lld below K, N",
-                                           (long long)ldx, (long long)ldy);
+  if (int e = check_linear("nf4_linear", x, M, K, ldx, packed, absmax, blocksize, code, N, bias, y, ldy, dtype))
+    return e;
   if (M == 0) return ok();
-  if (!x || !packed || !absmax || !y || !code) return set_error(SELAS_EINVAL, "nf4_linear: null pointer");
-  if (dtype != SELAS_BF16) return set_error(SELAS_EUNSUPPORTED, "nf4_linear: fused kernels take bf16, got %s",
-                                            dtype_name(dtype));
-  if (blocksize != 64 || K % 64) return set_error(SELAS_EUNSUPPORTED,
-                                                  "nf4_linear: fused kernels need blocksize 64 and K %% 64 == 0 "
-                                                  "(blocksize %lld, K %lld)", (long long)blocksize, (long long)K);
-  if (!aligned(x, 16) || ldx % 8 || !aligned(packed, 16) || !aligned(absmax, 4) || !aligned(y, 8) || ldy % 4 ||
-      (bias && !aligned(bias, 2)))
-    return set_error(SELAS_EUNSUPPORTED, "nf4_linear: fused kernels need 16-byte aligned x rows and codes, "
-                                         "8-byte aligned y rows");
-  // Buffer offsets are 32-bit: every operand (plus one tile of overhang) must span < 4 GiB.
-  const int64_t lim = (1ll << 32) - 1;
-  if ((M + 512) * ldx * 2 > lim || (N + 256) * (K / 2) > lim || (N + 256) * (K / 64) * 4 > lim)
-    return set_error(SELAS_EUNSUPPORTED, "nf4_linear: operand above 4 GiB");
   Code16 c;
   for (int i = 0; i < 16; ++i) c.v[i] = code[i];
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1029,8 +1075,41 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
         xb, ldx, static_cast<int>(M), static_cast<int>(K), packed, absmax, c, static_cast<int>(N), bb, yb, ldy);
     return check_launch("nf4_linear (gemv)");
   }
-  launch_gemm<8, 2, 3>(xb, ldx, M, K, packed, absmax, c, N, bb, yb, ldy, s);
+  GemmBatch batch{};
+  batch.count = 1;
+  batch.p[0] = GemmProblem{xb, packed, absmax, bb, yb, ldx, ldy, static_cast<int>(M), static_cast<int>(K),
+                           static_cast<int>(N), 0, 0};
+  launch_gemm<8, 2, 3>(batch, c, s);
   return check_launch("nf4_linear (gemm)");
+}
+
+extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
+                                        const float code[16], int dtype, void *stream) {
+  static_assert(kGemmMaxProblems == SELAS_MAX_BATCHED_LINEARS, "batch size");
+  if (count < 0 || count > kGemmMaxProblems)
+    return set_error(SELAS_EINVAL, "nf4_linear_batched: count %lld outside [0, %d]", (long long)count,
+                     kGemmMaxProblems);
+  if (count > 0 && !problems) return set_error(SELAS_EINVAL, "nf4_linear_batched: null problems");
+  GemmBatch batch{};
+  for (int64_t i = 0; i < count; ++i) {
+    const selas_nf4_gemm_problem &q = problems[i];
+    if (int e = check_linear("nf4_linear_batched", q.x, q.M, q.K, q.ldx, q.packed, q.absmax, blocksize, code, q.N,
+                             q.bias, q.y, q.ldy, dtype))
+      return e;
+    if (q.M == 0) continue;
+    if (q.M <= 32)
+      return set_error(SELAS_EUNSUPPORTED, "nf4_linear_batched: M <= 32 runs the skinny kernel (M=%lld)",
+                       (long long)q.M);
+    batch.p[batch.count++] = GemmProblem{static_cast<const uint16_t *>(q.x), q.packed, q.absmax,
+                                         static_cast<const uint16_t *>(q.bias), static_cast<uint16_t *>(q.y), q.ldx,
+                                         q.ldy, static_cast<int>(q.M), static_cast<int>(q.K), static_cast<int>(q.N),
+                                         0, 0};
+  }
+  if (batch.count == 0) return ok();
+  Code16 c;
+  for (int i = 0; i < 16; ++i) c.v[i] = code[i];
+  launch_gemm<8, 2, 3>(batch, c, static_cast<hipStream_t>(stream));
+  return check_launch("nf4_linear_batched");
 }
 
 extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx,

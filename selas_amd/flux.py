@@ -74,6 +74,15 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor
     return out.transpose(1, 2).reshape(b, l, h * d)
 
 
+def _linear_pair(w, a, b):
+    """w.linear on two independent (x, prefix) inputs; one launch when ``w`` batches linears."""
+    many = getattr(w, "linear_many", None)
+    if many is None:
+        return w.linear(*a), w.linear(*b)
+    ya, yb = many([a, b])
+    return ya, yb
+
+
 def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kernels = FUSED):
     """img [B, Li, D] fp32, txt [B, Lt, D] fp32, mod [B, 12D] (img 6D | txt 6D)."""
     m = mod.float().unsqueeze(1).chunk(12, dim=-1)
@@ -81,8 +90,8 @@ def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k
     t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = m[6:]
     lt = txt.shape[1]
     f32 = torch.float32
-    iqkv = w.linear(k.mod_in(img, i_sh1, i_sc1, dt), "img_attn.qkv")
-    tqkv = w.linear(k.mod_in(txt, t_sh1, t_sc1, dt), "txt_attn.qkv")
+    iqkv, tqkv = _linear_pair(w, (k.mod_in(img, i_sh1, i_sc1, dt), "img_attn.qkv"),
+                              (k.mod_in(txt, t_sh1, t_sc1, dt), "txt_attn.qkv"))
     q, kk, v = k.qkv_double(tqkv, iqkv, w.get("txt_attn.norm.query_norm.scale", f32),
                             w.get("txt_attn.norm.key_norm.scale", f32), w.get("img_attn.norm.query_norm.scale", f32),
                             w.get("img_attn.norm.key_norm.scale", f32), cos, sin, cfg.heads, dt)
@@ -90,12 +99,14 @@ def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k
     a = attention(q, kk, v)
     del q, kk, v
     t_attn, i_attn = a[:, :lt], a[:, lt:]
-    img, h = k.gated_add_mod(img, i_g1, w.linear(i_attn, "img_attn.proj"), i_sh2, i_sc2, dt, guard)
-    h = w.linear(h, "img_mlp.0")
-    img = k.gated_add(img, i_g2, w.linear(k.gelu(h), "img_mlp.2"), guard)
-    txt, h = k.gated_add_mod(txt, t_g1, w.linear(t_attn, "txt_attn.proj"), t_sh2, t_sc2, dt, guard)
-    h = w.linear(h, "txt_mlp.0")
-    txt = k.gated_add(txt, t_g2, w.linear(k.gelu(h), "txt_mlp.2"), guard)
+    i_proj, t_proj = _linear_pair(w, (i_attn, "img_attn.proj"), (t_attn, "txt_attn.proj"))
+    img, hi = k.gated_add_mod(img, i_g1, i_proj, i_sh2, i_sc2, dt, guard)
+    txt, ht = k.gated_add_mod(txt, t_g1, t_proj, t_sh2, t_sc2, dt, guard)
+    del i_proj, t_proj
+    hi, ht = _linear_pair(w, (hi, "img_mlp.0"), (ht, "txt_mlp.0"))
+    oi, ot = _linear_pair(w, (k.gelu(hi), "img_mlp.2"), (k.gelu(ht), "txt_mlp.2"))
+    img = k.gated_add(img, i_g2, oi, guard)
+    txt = k.gated_add(txt, t_g2, ot, guard)
     return img, txt
 
 

@@ -11,6 +11,8 @@ GPU, by the bit-exact decode kernel) and a library GEMM runs.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn.functional as F
 
@@ -62,6 +64,55 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
 GROUPED_K = (1024, 2048, 3072)  # the grouped kernel keeps x in registers: K = 8 waves x 2, 4 or 6 blocks of 64
 GROUPED_MAX_M = 32
 GROUPED_MAX_WEIGHTS = 1023
+
+
+def nf4_linear_batched(problems) -> list[torch.Tensor]:
+    """``[nf4_linear(*p) for p in problems]`` with the tiled GEMMs in one launch.
+
+    ``problems``: (x, packed, absmax, blocksize, code, shape, bias) tuples, as for
+    ``nf4_linear``, with independent inputs (e.g. the image and text streams of a double
+    block, selas/models/flux.py:300-324). The tiles of all problems share the GPU, so a
+    small problem runs in the CUs a large one leaves idle. Each result has the bits of
+    its own ``nf4_linear`` call; when any problem is outside the tiled GEMM (rows <= 32,
+    unsupported shapes) they run one by one.
+    """
+    problems = list(problems)
+    if len(problems) <= 1:
+        return [nf4_linear(*p) for p in problems]
+    outs = []
+    for i in range(0, len(problems), _lib.MAX_BATCHED_LINEARS):
+        outs += _batched_chunk(problems[i:i + _lib.MAX_BATCHED_LINEARS])
+    return outs
+
+
+def _batched_chunk(problems):
+    codes = {tuple(float(c) for c in p[4]) for p in problems}
+    x0 = problems[0][0]
+    if len(codes) != 1 or any(p[0].dtype != torch.bfloat16 or int(p[3]) != 64 for p in problems):
+        return [nf4_linear(*p) for p in problems]
+    dev = _lib.require_gpu(*(p[0] for p in problems), *(p[1] for p in problems))
+    arr = (_lib.GemmProblem * len(problems))()
+    outs, keep = [], []
+    for i, (x, packed, absmax, _, _, shape, bias) in enumerate(problems):
+        n, k = int(shape[0]), int(shape[1])
+        if len(shape) != 2 or x.shape[-1] != k:
+            raise ValueError(f"x has {x.shape[-1]} features, weight {tuple(shape)} expects {k}")
+        x2 = _rows(x)
+        if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
+            bias = bias.to(x.dtype).contiguous()
+        y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+        keep += [x2, bias]
+        outs.append(y)
+        arr[i] = _lib.GemmProblem(x2.data_ptr(), x2.shape[0], k, x2.stride(0), packed.data_ptr(), absmax.data_ptr(), n,
+                                  _lib.ptr(bias), y.data_ptr(), n)
+    try:
+        with torch.cuda.device(dev):
+            _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), len(problems), 64,
+                      _lib.code_array(next(iter(codes))), _lib.BF16, _lib.stream(dev))
+    except _lib.Unsupported:
+        return [nf4_linear(*p) for p in problems]
+    del keep  # the launch is queued on the stream that later reuses this memory
+    return outs
 
 
 class GroupedPlan:
@@ -178,6 +229,20 @@ class UnitView:
         if e.codec == "raw" and out.data_ptr() == e.parts["data"].data_ptr():
             self._views[key] = out
         return out
+
+    def linear_many(self, items, dtype: torch.dtype | None = None) -> list[torch.Tensor]:
+        """``[self.linear(x, prefix) for x, prefix in items]``, NF4 tiled GEMMs in one launch."""
+        dtype = dtype or self.dtype
+        items = list(items)
+        probs = []
+        for x, prefix in items:
+            e = self.tensors[prefix + ".weight"]
+            if e.codec != "nf4" or x.dtype != dtype:
+                return [self.linear(x, p, dtype) for x, p in items]
+            bname = prefix + ".bias"
+            b = self.get(bname, dtype) if bname in self.tensors else None
+            probs.append((x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"], e.shape, b))
+        return nf4_linear_batched(probs)
 
     def linear(self, x: torch.Tensor, prefix: str, dtype: torch.dtype | None = None) -> torch.Tensor:
         dtype = dtype or self.dtype

@@ -181,3 +181,26 @@ def test_grouped_skinny_equals_one_by_one(dev):
             assert y.shape == alone.shape == (m, 1, w[4][0])
             assert torch.equal(y, alone)  # same bits as the per-linear call
             check_close(y.reshape(m, -1), oracle_linear(x.reshape(m, -1), w_ref, w[5]))
+
+
+def test_batched_equals_one_by_one(dev):
+    from selas_amd.linear import nf4_linear_batched
+
+    shapes = [(300, 256, 3072), (64, 192, 640), (512, 320, 1024), (100, 64, 64), (1000, 96, 128)]
+    probs, refs = [], []
+    for i, (m, n, k) in enumerate(shapes):
+        p, a, w_ref = make_weight(n, k, 70 + i, dev)
+        x = torch.randn(m, k, generator=seeded(80 + i)).to(torch.bfloat16).to(dev)
+        b = (torch.randn(n, generator=seeded(90 + i)) * 0.02).to(torch.bfloat16).to(dev) if i % 2 else None
+        probs.append((x, p, a, 64, codecs.NF4_CODE, (n, k), b))
+        refs.append(w_ref)
+    ys = nf4_linear_batched(probs)  # five problems: a launch of four, then one
+    for prob, w_ref, y in zip(probs, refs, ys):
+        assert torch.equal(y, nf4_linear(*prob))  # same bits as the call alone
+        check_close(y, oracle_linear(prob[0], w_ref, prob[6]))
+    # a skinny problem in the batch: everything runs one by one, same results
+    xs = torch.randn(8, 3072, generator=seeded(99)).to(torch.bfloat16).to(dev)
+    mixed = [probs[0], (xs,) + probs[0][1:]]
+    y0, y1 = nf4_linear_batched(mixed)
+    assert torch.equal(y0, nf4_linear(*probs[0])) and torch.equal(y1, nf4_linear(*mixed[1]))
+

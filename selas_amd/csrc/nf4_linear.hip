@@ -201,57 +201,65 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
 
 // ------------------------------------------------------------- streaming skinny GEMM
 //
-// For M <= 32 and K = 512 * BPW (BPW = 2, 4, 6: K = 1024, 2048, 3072; the
-// hoisted modulation linears have K = hidden = 3072). One 512-thread
-// workgroup per CU streams 32-row slabs ("units") of one or many weights.
+// For M <= 32 and K = 1024, 2048, 3072 (the hoisted modulation linears have
+// K = hidden = 3072). One workgroup of NW waves per CU streams 32-row slabs
+// ("units") of one or many weights.
 //
-//   * Wave w owns the K slice of blocks [w*BPW, (w+1)*BPW) and keeps x for that
-//     slice in registers for the whole launch (A fragments, rows past M repeat
-//     row M-1).
+//   * Wave w owns the K slice of blocks [w*BPW, (w+1)*BPW) (K = 64*NW*BPW) and
+//     keeps x for that slice in registers for the whole launch, as fp16 MFMA
+//     A fragments (rows past M repeat row M-1).
 //   * Each wave copies its slice of the unit's codes (32 rows x BPW*32 bytes)
 //     from HBM into its own LDS stage with buffer-load-to-LDS DMA; the unit's
 //     scales (32 rows x K/64 floats, one contiguous block) are copied by the
-//     first BPW waves into a shared double buffer. Consecutive lanes fetch
+//     waves together into a shared double buffer. Consecutive lanes fetch
 //     consecutive 16-byte chunks, so every request covers whole cache lines;
 //     the chunk order inside a code row is XOR-swizzled so that the MFMA-order
 //     reads (lane (c, h) reads row c) are free of bank conflicts.
 //   * Once its codes are in registers a wave issues the next unit's DMA and
-//     multiplies: each code byte is looked up in a 32-way replicated LDS table
-//     of (hi, lo) bf16 pairs (one v_perm for the address, one ds_read_b64),
-//     fed to two MFMAs, and the fp32 block sums are scaled by absmax.
-//   * The eight partial results of a unit are summed in LDS in wave order
+//     multiplies: each code byte is looked up in a 64-way replicated LDS table
+//     of fp16 code pairs (one v_perm for the address, one ds_read_b32), four
+//     lookups make the B operand of one v_mfma_f32_32x32x16_f16, and the fp32
+//     block sums are scaled by absmax.
+//   * The NW partial results of a unit are summed in LDS in wave order
 //     (deterministic). Every wave drains its DMAs before the barrier that
-//     precedes the partial-sum stores, so after that barrier the next unit's
-//     codes and scales are in LDS for everyone. The sum and the bf16 stores of
-//     unit u run after the DMA of unit u+2 has been issued.
+//     follows the partial-sum stores, so after it the next unit's codes and
+//     scales are in LDS for everyone. With 4 waves the partial sums are double
+//     buffered and a unit needs that one barrier; with 8 a second barrier
+//     guards the single buffer. The sum and the bf16 stores of unit u run
+//     during unit u+1, before its DMA is issued.
 
-constexpr int kSgThreads = 512, kSgWaves = 8, kSgRows = 32;
-constexpr int kSgTableBytes = 256 * 64 * 4;            // [byte][lane] -> fp16 code pair
-constexpr int kSgRedBytes = kSgWaves * 16 * 64 * 4;   // [wave][r][lane] partial sums
+constexpr int kSgRows = 32;
+constexpr int kSgTableBytes = 256 * 64 * 4;  // [byte][lane] -> fp16 code pair
 constexpr int kSgMaxDescs = 1023;
 #ifndef SG_AHEAD
 #define SG_AHEAD 1
 #endif
 constexpr int kSgAhead = SG_AHEAD;  // sub-steps of table lookups in flight
-#ifndef SG_SPREAD
-#define SG_SPREAD 0
+#ifndef SG_WAVES
+#define SG_WAVES 8
 #endif
-constexpr bool kSgSpread = SG_SPREAD;  // DMA instructions spread over the compute blocks
+constexpr int kSgWaves = SG_WAVES;  // waves per workgroup (8: two per SIMD; 4 measured 25 % slower)
 
-template <int BPW>
+template <int NW, int BPW>
 struct SgLayout {
+  static constexpr int kThreads = 64 * NW;
   // A wave's slice of a code row is kChunks 16-byte chunks; the 32 rows of a unit
   // are kCodeInstrs DMA instructions of 64 chunks.
   static constexpr int kChunks = 2 * BPW;
   static constexpr int kCodeInstrs = BPW;
   static constexpr int kCodeBytes = kSgRows * kChunks * 16;
-  static constexpr int kScaleBytes = kSgRows * 8 * BPW * 4;      // a unit's scales: BPW DMA instructions of 1 KiB
-  static constexpr int kStage = kSgTableBytes;                   // byte offsets in dynamic LDS
-  static constexpr int kScales = kStage + kSgWaves * kCodeBytes;  // two buffers
+  static constexpr int kBlocks = NW * BPW;                         // K / 64
+  static constexpr int kScaleBytes = kSgRows * kBlocks * 4;        // a unit's scales
+  static constexpr int kScaleInstrs = kScaleBytes / 1024;          // DMA instructions of 1 KiB
+  static constexpr int kRedBufs = NW == 4 ? 2 : 1;
+  static constexpr int kRedBytes = kRedBufs * NW * 16 * 64 * 4;   // [buf][wave][r][lane] partial sums
+  static constexpr int kStage = kSgTableBytes;                     // byte offsets in dynamic LDS
+  static constexpr int kScales = kStage + NW * kCodeBytes;         // two buffers
   static constexpr int kRed = kScales + 2 * kScaleBytes;
-  static constexpr int kPrefix = kRed + kSgRedBytes;
+  static constexpr int kPrefix = kRed + kRedBytes;
   static constexpr int kMaxBytes = kPrefix + (kSgMaxDescs + 1) * 4;
-  static_assert(BPW % 2 == 0 && BPW <= 6, "slice of 2, 4 or 6 blocks per wave");
+  static constexpr int kOuts = 1024 / kThreads;                    // outputs of a 32x32 unit tile per thread
+  static_assert(kScaleBytes % 1024 == 0 && kChunks % 4 == 0, "layout");
   static_assert(kMaxBytes <= 160 * 1024, "LDS");
 };
 
@@ -290,15 +298,22 @@ __device__ __forceinline__ void load_lds16_at(__amdgpu_buffer_rsrc_t r, void *ld
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, 0, 0, 0);
 }
 
-// XOR applied to the chunk index of row r inside a wave's code stage.
-__device__ __forceinline__ int sg_swz(int r) { return (r >> 2) & 3; }
+// XOR applied to the chunk index of row r inside a wave's code stage: chosen
+// so that 16 consecutive rows, read at one chunk, hit 16 distinct 16-byte bank
+// groups (a row is kChunks*16 bytes; 64 banks of 4 bytes).
+template <int kChunks>
+__device__ __forceinline__ int sg_swz(int r) {
+  if constexpr (kChunks % 16 == 0) return r & 15;
+  else if constexpr (kChunks % 8 == 0) return (r >> 1) & 7;
+  else return (r >> 2) & 3;
+}
 
-template <int BPW>
-__global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
+template <int NW, int BPW>
+__global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     const uint16_t *__restrict__ x, int64_t ldx, int M, const GemvDesc *__restrict__ descs, int count,
     GemvDesc one, Code16 code) {
-  using L = SgLayout<BPW>;
-  constexpr int K = 512 * BPW, kblocks = 8 * BPW, row_bytes = K / 2;
+  using L = SgLayout<NW, BPW>;
+  constexpr int kblocks = L::kBlocks, K = 64 * kblocks, row_bytes = K / 2, kThreads = L::kThreads;
   extern __shared__ __align__(16) uint32_t lds_words[];
   uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
   int *prefix = reinterpret_cast<int *>(lds + L::kPrefix);
@@ -332,11 +347,12 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
   __syncthreads();
   {
     // Entry (b, j) at b*256 + 4*j: fp16 pair (code[b >> 4], code[b & 15]), one replica per lane j.
+    constexpr int kParts = kThreads / 256, kPer = 64 / kParts;
     const int b = tid & 255, part = tid >> 8;
     const uint32_t e = code16[b >> 4] | (code16[b & 15] << 16);
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int r = 32 * part + ((j + lane) & 31);
+    for (int j = 0; j < kPer; ++j) {
+      const int r = kPer * part + ((j + lane) & (kPer - 1));
       *reinterpret_cast<uint32_t *>(lds + b * 256 + r * 4) = e;
     }
   }
@@ -344,11 +360,6 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
   // x fragments of this wave's slice: block b, sub-step s covers k = 64*(kb0+b) + 32h + 8s .. +8.
   const int kb0 = wave * BPW;
   const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 64 * kb0 + 32 * h;
-  uint4 xb[BPW][4];
-#pragma unroll
-  for (int b = 0; b < BPW; ++b)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) xb[b][s] = *reinterpret_cast<const uint4 *>(xr + 64 * b + 8 * s);
   // Row maxima of |x| (as bf16 magnitude bits: ordered like the values, NaN above Inf).
   {
     uint32_t mx = 0;
@@ -356,7 +367,8 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
     for (int b = 0; b < BPW; ++b)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint32_t w[4] = {xb[b][s].x, xb[b][s].y, xb[b][s].z, xb[b][s].w};
+        const uint4 q = *reinterpret_cast<const uint4 *>(xr + 64 * b + 8 * s);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
       }
@@ -366,7 +378,7 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
 
   uint8_t *stage = lds + L::kStage + wave * L::kCodeBytes;
   // MFMA-order reads: lane (c, h) takes chunk 2b + h of row c.
-  const int rd_base = c * L::kChunks * 16, rd_swz = sg_swz(c);
+  const int rd_base = c * L::kChunks * 16, rd_swz = sg_swz<L::kChunks>(c);
   // v_perm source for table addresses: byte 0 = 4 * lane, byte 1 <- code byte.
   const uint32_t tsel = static_cast<uint32_t>(lane) * 4u;
 
@@ -392,7 +404,8 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
     for (int b = 0; b < BPW; ++b)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint32_t w[4] = {xb[b][s].x, xb[b][s].y, xb[b][s].z, xb[b][s].w};
+        const uint4 q = *reinterpret_cast<const uint4 *>(xr + 64 * b + 8 * s);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           xf[b][s][2 * i] = static_cast<_Float16>(__uint_as_float(w[i] << 16) * sc);
@@ -400,11 +413,11 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
         }
       }
   }
-  // Inverse scales of the two output rows this thread finishes (fixed for the launch).
-  float inv_m[2];
+  // Inverse scales of the output rows this thread finishes (fixed for the launch).
+  float inv_m[L::kOuts];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = wave + 8 * i;
+  for (int i = 0; i < L::kOuts; ++i) {
+    const int r = wave + NW * i;
     inv_m[i] = row_scale(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), true);
   }
 
@@ -421,24 +434,26 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
   // Descriptors are uniform: kept in scalar registers and reloaded only when the weight changes.
   auto desc = [&](int g) { return uniform_desc(descs ? descs[g] : one); };
   auto scales = [&](int u) { return reinterpret_cast<float *>(lds + L::kScales + ((u - u_begin) & 1) * L::kScaleBytes); };
-  // DMA instruction j of unit u's codes; j == 0 also fetches this wave's share of the scales.
   // Code instruction j fetches chunk (p ^ swz(r)) of row r into stage slot
-  // 64j + lane = r*kChunks + p. The buffers start at the unit's first row, so
-  // rows past the weight's end fall outside their ranges and read as 0.
-  auto issue_part = [&](int j, int u, const SDesc &d, int row0) {
-    const uint32_t q = 64u * j + lane, r = q / L::kChunks, p = q - r * L::kChunks;
+  // 64j + lane = r*kChunks + p; scale instructions j = wave, wave + NW, ... fetch
+  // 1 KiB each. The buffers start at the unit's first row, so rows past the
+  // weight's end fall outside their ranges and read as 0.
+  auto issue = [&](int u, const SDesc &d, int row0) {
     const auto rc = make_rsrc(d.packed + static_cast<int64_t>(row0) * row_bytes,
                               static_cast<uint32_t>(max(d.n - row0, 0)) * row_bytes);
-    load_lds16_at(rc, stage + 1024 * j, r * row_bytes + 32 * kb0 + 16 * (p ^ sg_swz(r)));
-    if (j == 0 && wave < BPW) {
-      const auto ra = make_rsrc(d.absmax + static_cast<int64_t>(row0) * kblocks,
-                                static_cast<uint32_t>(max(d.n - row0, 0)) * (kblocks * 4));
-      load_lds16_at(ra, reinterpret_cast<uint8_t *>(scales(u)) + 1024 * wave, 1024 * wave + 16 * lane);
-    }
-  };
-  auto issue = [&](int u, const SDesc &d, int row0) {
 #pragma unroll
-    for (int j = 0; j < L::kCodeInstrs; ++j) issue_part(j, u, d, row0);
+    for (int j = 0; j < L::kCodeInstrs; ++j) {
+      const uint32_t q = 64u * j + lane, r = q / L::kChunks, p = q - r * L::kChunks;
+      load_lds16_at(rc, stage + 1024 * j, r * row_bytes + 32 * kb0 + 16 * (p ^ sg_swz<L::kChunks>(r)));
+    }
+    const auto ra = make_rsrc(d.absmax + static_cast<int64_t>(row0) * kblocks,
+                              static_cast<uint32_t>(max(d.n - row0, 0)) * (kblocks * 4));
+#pragma unroll
+    for (int jj = 0; jj < (L::kScaleInstrs + NW - 1) / NW; ++jj) {
+      const int j = wave + NW * jj;
+      if (j < L::kScaleInstrs)
+        load_lds16_at(ra, reinterpret_cast<uint8_t *>(scales(u)) + 1024 * j, 1024 * j + 16 * lane);
+    }
   };
   // Bias and outputs go through buffer resources, not generic pointers: a
   // flat access might touch LDS and would make every later LDS read wait for
@@ -450,20 +465,22 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
     const auto rb = make_rsrc(d.bias, static_cast<uint32_t>(d.n * 2));
     return __builtin_amdgcn_raw_buffer_load_b16(rb, static_cast<uint32_t>(n) * 2u, 0, 0);
   };
-  // Sum of the eight partials of the unit held in `red`, plus bias, to bf16.
-  // Half i of the outputs of the unit whose partials are in `red`.
-  auto finish = [&](int i, const SDesc &d, int row0, uint32_t bias_bits) {
+  // The outputs this thread owns of the unit whose partials are in buffer `buf`:
+  // the NW partials summed in wave order, bias added, rounded to bf16.
+  auto finish = [&](int buf, const SDesc &d, int row0, uint32_t bias_bits) {
     const int N = d.n;
     const float bv = bf16_bits_to_f32(static_cast<uint16_t>(bias_bits));
     const auto ry = make_rsrc(d.y, static_cast<uint32_t>(((M - 1) * d.ldy + N) * 2));
-    {
-      const int e = tid + kSgThreads * i;
+    const float *rb = red + buf * NW * 1024;
+#pragma unroll
+    for (int i = 0; i < L::kOuts; ++i) {
+      const int e = tid + kThreads * i;
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kSgWaves; ++w) v += red[w * 1024 + e];
-      const int l = e & 63, r = e >> 6;
-      const int m = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      const int n = row0 + (l & 31);
+      for (int w = 0; w < NW; ++w) v += rb[w * 1024 + e];
+      const int r = e >> 6;
+      const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+      const int n = row0 + c;
       if (m < M && n < N)
         __builtin_amdgcn_raw_buffer_store_b16(bf16_bits_rne(v * inv_m[i] + bv), ry,
                                               static_cast<uint32_t>(m * d.ldy + n) * 2u, 0, 0);
@@ -494,6 +511,7 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
   int row_prev = row_cur;
   uint32_t bias_prev = 0;
   for (int u = u_begin; u < u_end; ++u) {
+    const int buf = (u - u_begin) & (L::kRedBufs - 1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage read before the next DMA overwrites it
     const uint32_t bias_cur = load_bias(d_cur, row_cur);
     int g_nxt = g_cur, row_nxt = row_cur + kSgRows;
@@ -504,11 +522,8 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
       d_nxt = desc(g_nxt);
       row_nxt = (u + 1 - prefix[g_nxt]) * kSgRows;
     }
-    if (u > u_begin) {  // partials of unit u-1 (barrier at the end of u-1)
-      finish(0, d_prev, row_prev, bias_prev);
-      finish(1, d_prev, row_prev, bias_prev);
-    }
-    if (!kSgSpread && more) issue(u + 1, d_nxt, row_nxt);
+    if (u > u_begin) finish(buf ^ (L::kRedBufs - 1), d_prev, row_prev, bias_prev);  // unit u-1
+    if (more) issue(u + 1, d_nxt, row_nxt);
 
     // Table lookups run kSgAhead sub-steps ahead of the MFMAs that use them.
     auto word = [&](int t) {
@@ -530,11 +545,6 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
       f32x16 p = f32x16{};
-      if (kSgSpread && more) {  // this block's share of the next unit's DMA instructions
-#pragma unroll
-        for (int j = b * L::kCodeInstrs / BPW; j < (b + 1) * L::kCodeInstrs / BPW; ++j)
-          issue_part(j, u + 1, d_nxt, row_nxt);
-      }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int t = 4 * b + s;
@@ -549,11 +559,19 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
       for (int r = 0; r < 16; ++r) acc[r] += p[r] * a[b];
     }
     wait_vmcnt<0>();  // this wave's DMAs of unit u+1 have landed
-    __syncthreads();  // ... everyone's, and every wave has summed unit u-1 from `red`
+    float *rw = red + buf * NW * 1024;
+    if constexpr (L::kRedBufs == 1) {
+      __syncthreads();  // every wave has summed unit u-1 from the single buffer
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
-    if (u + 1 < u_end) read_stage(u + 1);  // its latency overlaps the barrier
-    __syncthreads();
+      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r];
+      if (more) read_stage(u + 1);  // its latency overlaps the barrier
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r];
+      __syncthreads();  // partials of unit u complete; every wave's DMAs of unit u+1 landed
+      if (more) read_stage(u + 1);
+    }
     d_prev = d_cur;
     row_prev = row_cur;
     bias_prev = bias_cur;
@@ -561,8 +579,7 @@ __global__ __launch_bounds__(kSgThreads, 1) void nf4_gemv_stream(
     d_cur = d_nxt;
     row_cur = row_nxt;
   }
-  finish(0, d_prev, row_prev, bias_prev);
-  finish(1, d_prev, row_prev, bias_prev);
+  finish((u_end - 1 - u_begin) & (L::kRedBufs - 1), d_prev, row_prev, bias_prev);
 }
 
 int cu_count() {
@@ -578,19 +595,19 @@ int cu_count() {
 // True when the streaming kernel covers K.
 bool stream_k(int64_t K) { return K == 1024 || K == 2048 || K == 3072; }
 
-template <int BPW>
+template <int NW, int BPW>
 int launch_stream(const uint16_t *x, int64_t ldx, int64_t M, const GemvDesc *descs, int count, const GemvDesc &one,
                   int64_t total_n, const Code16 &c, hipStream_t s) {
-  using L = SgLayout<BPW>;
+  using L = SgLayout<NW, BPW>;
   const int64_t units = cdiv(total_n, kSgRows) + count;
   const int64_t grid = min(units, static_cast<int64_t>(cu_count()));
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_gemv_stream<BPW>),
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_gemv_stream<NW, BPW>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, L::kMaxBytes);
   if (attr != hipSuccess)
     return set_error(SELAS_EHIP, "nf4_linear: cannot reserve %d bytes of LDS: %s", L::kMaxBytes,
                      hipGetErrorString(attr));
   const size_t lds = L::kPrefix + (count + 1) * sizeof(int);
-  nf4_gemv_stream<BPW><<<dim3(static_cast<uint32_t>(grid)), dim3(kSgThreads), lds, s>>>(
+  nf4_gemv_stream<NW, BPW><<<dim3(static_cast<uint32_t>(grid)), dim3(L::kThreads), lds, s>>>(
       x, ldx, static_cast<int>(M), descs, count, one, c);
   return check_launch("nf4_linear (streaming skinny gemm)");
 }
@@ -598,10 +615,11 @@ int launch_stream(const uint16_t *x, int64_t ldx, int64_t M, const GemvDesc *des
 // total_n: sum of the weights' row counts (an upper bound on the work, for the grid size).
 int launch_gemv_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const GemvDesc *descs, int count,
                        const GemvDesc &one, int64_t total_n, const Code16 &c, hipStream_t s) {
+  constexpr int NW = kSgWaves;
   switch (K) {
-    case 1024: return launch_stream<2>(x, ldx, M, descs, count, one, total_n, c, s);
-    case 2048: return launch_stream<4>(x, ldx, M, descs, count, one, total_n, c, s);
-    case 3072: return launch_stream<6>(x, ldx, M, descs, count, one, total_n, c, s);
+    case 1024: return launch_stream<NW, 1024 / 64 / NW>(x, ldx, M, descs, count, one, total_n, c, s);
+    case 2048: return launch_stream<NW, 2048 / 64 / NW>(x, ldx, M, descs, count, one, total_n, c, s);
+    case 3072: return launch_stream<NW, 3072 / 64 / NW>(x, ldx, M, descs, count, one, total_n, c, s);
     default: return set_error(SELAS_EUNSUPPORTED, "nf4_linear: streaming skinny kernel takes K = 1024, 2048, 3072");
   }
 }

@@ -87,9 +87,19 @@ class Timer:
         e1.record()
         self.pairs.setdefault(name, []).append((e0, e1))
 
+    def times_ms(self, name):
+        return [a.elapsed_time(b) for a, b in self.pairs.get(name, [])]
+
     def mean_ms(self, name):
-        ps = self.pairs.get(name, [])
-        return sum(a.elapsed_time(b) for a, b in ps) / max(1, len(ps))
+        ts = self.times_ms(name)
+        return sum(ts) / max(1, len(ts))
+
+    def median_ms(self, name):
+        ts = sorted(self.times_ms(name))
+        if not ts:
+            return 0.0
+        n = len(ts)
+        return ts[n // 2] if n % 2 else 0.5 * (ts[n // 2 - 1] + ts[n // 2])
 
 
 # --------------------------------------------------------------------------- config 2 (the value)
@@ -117,11 +127,14 @@ def bench_block_linears(dev, steps, warmup, copies=8):
         tm.stop(t)
     torch.cuda.synchronize(dev)
     wall = (time.perf_counter() - t0) / steps
+    # The roofline figure uses the mean launch time (what a kernel trace's average reports); the
+    # medians are listed beside it.
     k1, k2 = tm.mean_ms("linear1"), tm.mean_ms("linear2")
     nbytes = sum(e.nbytes for e in (w1[0], w2[0]))
     return {
         "flop_per_step": f1 + f2, "ms_per_step": wall * 1e3,
         "kernel_ms": {"linear1": k1, "linear2": k2},
+        "kernel_ms_median": {"linear1": tm.median_ms("linear1"), "linear2": tm.median_ms("linear2")},
         "kernel_tflops": {"linear1": f1 / k1 / 1e9, "linear2": f2 / k2 / 1e9},
         "achieved_tflops": (f1 + f2) / (k1 + k2) / 1e9,
         "nf4_bytes_per_step": nbytes,
@@ -145,7 +158,7 @@ def bench_single_linear(dev, steps, warmup):
         lin(x, ws[i % 8])
         tm.stop(t)
     torch.cuda.synchronize(dev)
-    ms = tm.mean_ms("l")
+    ms = tm.median_ms("l")
     return {"shape": [m, n, k], "kernel_ms": ms, "tflops": 2.0 * m * n * k / ms / 1e9}
 
 
@@ -181,7 +194,7 @@ def bench_library_path(dev, steps, warmup):
         torch.nn.functional.linear(x2, b)
         tm.stop(t)
     torch.cuda.synchronize(dev)
-    g = tm.mean_ms("g")
+    g = tm.median_ms("g")
     return {"ms_per_step": ms, "tflops": f / ms / 1e9, "gemm_only_ms": g, "gemm_only_tflops": f / g / 1e9}
 
 
@@ -227,9 +240,9 @@ def bench_modulations(dev, steps, warmup):
         plan.run(x)
         tm.stop(t)
     torch.cuda.synchronize(dev)
-    per = tm.mean_ms("gemv")
-    grp = tm.mean_ms("grouped_kernel")
-    call = tm.mean_ms("grouped_call")
+    per = tm.median_ms("gemv")
+    grp = tm.median_ms("grouped_kernel")
+    call = tm.median_ms("grouped_call")
     return {"launches": 76, "bytes": nbytes, "flops": flops, "grouped_kernel_ms": grp,
             "gbs_grouped": nbytes / grp / 1e6, "frac_hbm_grouped": nbytes / grp / 1e6 / PEAK_HBM_GBS,
             "grouped_call_ms": call, "per_linear_kernel_ms_mean": per, "gbs_per_linear": nbytes / (per * 76) / 1e6}
@@ -270,12 +283,32 @@ def bench_segments(dev, steps, warmup):
             fn()
             tm.stop(t)
         torch.cuda.synchronize(dev)
-        ms = tm.mean_ms(name)
+        ms = tm.median_ms(name)
         out[name] = {"bytes": nb, "kernel_ms": ms, "gbs": nb / ms / 1e6, "frac_hbm": nb / ms / 1e6 / PEAK_HBM_GBS}
     return out
 
 
-def bench_full_step(dev, steps, warmup):
+def segment_bytes(kind: str, cfg, l_img: int, l_txt: int, batch: int) -> float:
+    """HBM bytes the fused segments of one block move per step (each tensor read or written once).
+
+    Per token, D = hidden, F = mlp_hidden, Dh = head dim: mod_in reads x fp32 and writes bf16 (6D);
+    attention prep reads q, k, v bf16 and writes them (12D) plus cos/sin (4 Dh); gated_add reads
+    x fp32 and y bf16 and writes fp32 (10D); gated_add_mod also writes h bf16 (12D); gelu reads and
+    writes F bf16 (4F); attn_mlp reads attn and mlp and writes the concat (4D + 4F)."""
+    d, f, dh = cfg.hidden, cfg.mlp_hidden, cfg.hidden // cfg.heads
+    tok = batch * (l_img + l_txt)
+    if kind == "double":
+        return tok * (6 * d + 12 * d + 4 * dh + 12 * d + 4 * f + 10 * d)
+    if kind == "single":
+        return tok * (6 * d + 12 * d + 4 * dh + 4 * d + 4 * f + 10 * d)
+    return 0.0
+
+
+def bench_full_step(dev, steps, warmup, batch=1, res=1024):
+    """FLUX-dev-shaped step (19 double + 38 single blocks, all NF4 weights resident) at res^2 with
+    `batch` images. Each image's 28-step modulations come from its own grouped skinny launch (outside
+    the step time, as in the reference). Reports the median step time and the lower bound
+    linear FLOP / peak + attention FLOP / peak + segment bytes / HBM peak."""
     from selas_amd import flux as F
 
     cfg = F.FluxConfig()
@@ -285,32 +318,44 @@ def bench_full_step(dev, steps, warmup):
     build_s = time.perf_counter() - t0
     g = torch.Generator(device=dev).manual_seed(5)
     n_steps = 28
-    sv = torch.nn.functional.silu(torch.randn(n_steps, 1, D, generator=g, device=dev)).to(torch.bfloat16)
+    svs = [torch.nn.functional.silu(torch.randn(n_steps, 1, D, generator=g, device=dev)).to(torch.bfloat16)
+           for _ in range(batch)]
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    mods = model.modulations(sv)
+    per_image = [model.modulations(sv) for sv in svs]
     torch.cuda.synchronize(dev)
-    prologue_s = time.perf_counter() - t0
-    lt, grid = 512, 64
-    txt = torch.randn(1, lt, D, generator=g, device=dev)
-    lat = torch.randn(1, grid * grid, 64, generator=g, device=dev)
-    fmod = (torch.randn(1, 2 * D, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    prologue_s = (time.perf_counter() - t0) / batch
+    mods = [torch.cat([m[j] for m in per_image], dim=1) for j in range(len(per_image[0]))]  # [S, B, kD]
+    lt, grid = 512, res // 16
+    txt = torch.randn(batch, lt, D, generator=g, device=dev)
+    lat = torch.randn(batch, grid * grid, 64, generator=g, device=dev)
+    fmod = (torch.randn(batch, 2 * D, generator=g, device=dev) * 0.1).to(torch.bfloat16)
     ids = torch.cat((torch.zeros(lt, 3, device=dev), F.image_ids(grid, grid, dev)), dim=0)
     cos, sin = F.rope_tables(ids, cfg.axes_dim, cfg.theta)
     for s in range(warmup):
         model.step(lat, txt, [m[s] for m in mods], fmod, cos, sin)
     torch.cuda.synchronize(dev)
+    tm = Timer()
     t0 = time.perf_counter()
     for s in range(steps):
+        t = tm.start("step")
         v = model.step(lat, txt, [m[s % n_steps] for m in mods], fmod, cos, sin)
+        tm.stop(t)
     torch.cuda.synchronize(dev)
-    step_s = (time.perf_counter() - t0) / steps
+    wall_s = (time.perf_counter() - t0) / steps
+    step_s = tm.median_ms("step") / 1e3
     assert torch.isfinite(v).all()
-    lin_f = sum(F.unit_flops(kd, cfg, grid * grid, lt, 1)[0] * n for kd, n in (("double", 19), ("single", 38)))
-    att_f = sum(F.unit_flops(kd, cfg, grid * grid, lt, 1)[1] * n for kd, n in (("double", 19), ("single", 38)))
-    return {"s_per_step": step_s, "tflops": (lin_f + att_f) / step_s / 1e12, "linear_tflop": lin_f / 1e12,
-            "attention_tflop": att_f / 1e12, "prologue_s": prologue_s, "build_s": build_s,
-            "nf4_resident_gb": model.nf4_bytes() / 1e9}
+    li = grid * grid
+    blocks = (("double", 19), ("single", 38))
+    lin_f = sum(F.unit_flops(kd, cfg, li, lt, batch)[0] * n for kd, n in blocks)
+    att_f = sum(F.unit_flops(kd, cfg, li, lt, batch)[1] * n for kd, n in blocks)
+    seg_b = sum(segment_bytes(kd, cfg, li, lt, batch) * n for kd, n in blocks) + batch * li * 6 * D
+    bound_s = (lin_f + att_f) / (PEAK_BF16_TFLOPS * 1e12) + seg_b / (PEAK_HBM_GBS * 1e9)
+    return {"batch": batch, "resolution": res, "tokens_per_image": li + lt, "steps": steps,
+            "s_per_step": step_s, "s_per_step_wall": wall_s, "tflops": (lin_f + att_f) / step_s / 1e12,
+            "linear_tflop": lin_f / 1e12, "attention_tflop": att_f / 1e12, "segment_gb": seg_b / 1e9,
+            "lower_bound_s": bound_s, "frac_of_bound": bound_s / step_s,
+            "prologue_s_per_image": prologue_s, "build_s": build_s, "nf4_resident_gb": model.nf4_bytes() / 1e9}
 
 
 # --------------------------------------------------------------------------- CPU baseline
@@ -392,9 +437,10 @@ def copy_calibration(dev, gib: float = 1.0, reps: int = 3):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--full-step", action="store_true", help="also time the full FLUX-dev-shaped step at 1024^2")
+    ap.add_argument("--no-full-step", action="store_true",
+                    help="skip the full FLUX-dev-shaped steps (batch 1 at 1024^2, batch 4 at 512^2)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-calibration", action="store_true",
@@ -421,9 +467,13 @@ def main():
         log(f"bench: segments {json.dumps({k: round(v['gbs']) for k, v in extra['segments_m4608'].items()})}")
         extra["library_path"] = bench_library_path(dev, a.steps, a.warmup)
         log(f"bench: library path {extra['library_path']['tflops']:.1f} TFLOP/s")
-    if a.full_step:
-        extra["full_step_1024"] = bench_full_step(dev, max(3, a.steps // 4), 2)
-        log(f"bench: full step {extra['full_step_1024']['s_per_step']:.3f} s")
+    if not a.no_full_step:
+        fs_steps = max(3, a.steps // 5)
+        for key, batch, res_px in (("full_step_1024_b1", 1, 1024), ("full_step_512_b4", 4, 512)):
+            extra[key] = bench_full_step(dev, fs_steps, 2, batch, res_px)
+            r = extra[key]
+            log(f"bench: full step B{batch} at {res_px}^2: {r['s_per_step']:.4f} s/step "
+                f"(lower bound {r['lower_bound_s']:.4f} s, {100 * r['frac_of_bound']:.0f} %)")
     cpu = None if a.no_cpu else cpu_baseline()
     achieved = res["achieved_tflops"]
     line = {

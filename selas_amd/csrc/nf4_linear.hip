@@ -626,8 +626,6 @@ int launch_gemv_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, con
 
 // =========================================================================== GEMM (M > 32)
 
-constexpr int kGemmThreads = 256;
-
 // 16 bf16(code[i] * a) values as four byte planes (TL = low bytes, TH = high
 // bytes), entries 4j..4j+3 in plane register j. Lanes l and l+32 serve the
 // same (row, block); each computes eight products and the halves are
@@ -705,12 +703,15 @@ __device__ __forceinline__ void interleave_substep() {
   }
 }
 
-// Fused-dequant GEMM. A workgroup is 4 waves side by side along N; a wave owns
-// MB*32 rows x CB*32 columns of the output (MB*CB = 16 tiles of 32x32, 256
-// accumulator registers):
-//   MB=16, CB=1: 512 x 128 tile; each decoded weight serves 512 rows, which
-//                halves the decode work per MFMA; 2 LDS stages of 64 KiB.
-//   MB=8,  CB=2: 256 x 256 tile for small M; 3 LDS stages of 32 KiB.
+// Fused-dequant GEMM. A workgroup is NW waves side by side along N; a wave
+// owns MB*32 rows x CB*32 columns of the output (MB*CB tiles of 32x32, 16
+// accumulator registers each):
+//   MB=8, CB=2, NW=4: 256 x 256 tile, 256 accumulators, one wave per SIMD;
+//                     each decoded weight fragment serves 8 MFMAs.
+//   MB=4, CB=2, NW=8: 128 x 512 tile, 128 accumulators, two waves per SIMD
+//                     (one wave's waits overlap the other's MFMAs); each
+//                     decoded fragment serves 4 MFMAs.
+// Either way the workgroup reads 128 KiB of x fragments from LDS per K block.
 //
 // Grid: workgroup b runs on XCD b % 8; tile t = (b % 8) * per_xcd + b / 8
 // gives each XCD a contiguous range of tiles, column tile fastest, so that
@@ -741,13 +742,15 @@ struct GemmBatch {
   int count, tiles, per_xcd;
 };
 
-template <int MB, int CB, int STAGES>
-__global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
-  constexpr int TM = 32 * MB, WN = 32 * CB, TN = 4 * WN;
-  constexpr int SB = TM * 128;  // bytes of one x stage: TM rows x 64 bf16
+template <int MB, int CB, int STAGES, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
+  constexpr int TM = 32 * MB, WN = 32 * CB, TN = NW * WN;
+  constexpr int SB = TM * 128;      // bytes of one x stage: TM rows x 64 bf16
   constexpr int LOOK = STAGES - 1;
-  constexpr int LPB = 2 * CB + MB;  // vector-memory loads issued per K block and wave
-  static_assert(MB * CB == 16 && (STAGES == 2 || STAGES == 3), "tile shape");
+  constexpr int XL = 4 * MB / NW;   // x DMAs (8 rows each) per K block and wave
+  constexpr int LPB = 2 * CB + XL;  // vector-memory loads issued per K block and wave
+  static_assert(MB * CB * NW == 64 && (STAGES == 2 || STAGES == 3), "tile shape");
+  static_assert(XL % 2 == 0, "each wave's x rows start at a multiple of 16 (swizzle phase)");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB];
   const int t = (blockIdx.x & 7) * batch.per_xcd + (blockIdx.x >> 3);
   if (t >= batch.tiles) return;
@@ -777,19 +780,20 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(packed, static_cast<uint32_t>(N) * static_cast<uint32_t>(K >> 1));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(absmax, static_cast<uint32_t>(N) * static_cast<uint32_t>(kblocks) * 4u);
 
-  // x tile DMA: wave w fills tile rows [8*MB*w, 8*MB*(w+1)) with MB loads of 8
-  // rows; lane i of load j lands at row r = 8*MB*w + 8j + i/8, physical
+  // x tile DMA: wave w fills tile rows [8*XL*w, 8*XL*(w+1)) with XL loads of 8
+  // rows; lane i of load j lands at row r = 8*XL*w + 8j + i/8, physical
   // 16-byte chunk i%8, and so fetches logical chunk (i%8) ^ ((r/2)%8). With
   // that swizzle the 16 lanes one LDS cycle serves in a fragment read (16
   // consecutive rows, one logical chunk) hit 16 distinct 4-bank groups of the
-  // 64 banks. (r/2)%8 = (4j + i/16) % 8 depends on j only through its parity.
+  // 64 banks. With XL even, (r/2)%8 = (4j + i/16) % 8 depends on j only
+  // through its parity.
   uint32_t a_voff[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par)
-    a_voff[par] = static_cast<uint32_t>(m0 + 8 * MB * wave + (lane >> 3)) * ldx_b +
+    a_voff[par] = static_cast<uint32_t>(m0 + 8 * XL * wave + (lane >> 3)) * ldx_b +
                   (static_cast<uint32_t>((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 4);
   const uint32_t a_vstep = 8u * ldx_b;
-  uint8_t *const a_dst = smem + wave * MB * 1024;
+  uint8_t *const a_dst = smem + wave * XL * 1024;
   // Weight rows of this wave: n0 + WN*wave + 32*cb + c.
   uint32_t b_voff[CB], s_voff[CB];
 #pragma unroll
@@ -817,14 +821,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
     }
     uint8_t *dst = a_dst + stage * SB;
 #pragma unroll
-    for (int j = 0; j < MB; ++j) load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
+    for (int j = 0; j < XL; ++j) load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
   };
   // The same loads in four parts, one per sub-step, so that a wave never
   // queues a whole block's loads at once (issue would stall on the address
   // unit instead of overlapping the MFMAs): part 0 the codes, scales and the
-  // first x loads, parts 1-3 the rest of the x tile.
-  constexpr int XPP = MB / 4;                 // x loads per part
-  constexpr int P3 = XPP;                     // loads in part 3
+  // first x loads, parts 1-3 the rest of the x tile (x load j in part 4j/XL).
+  constexpr int P3 = XL - (3 * XL + 3) / 4;  // x loads in part 3
   auto issue_part = [&](int stage, int blk, int part, uint4 (&bq)[CB], float (&bs)[CB]) {
     const uint32_t kb = static_cast<uint32_t>(blk);
     if (part == 0) {
@@ -836,7 +839,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
     }
     uint8_t *dst = a_dst + stage * SB;
 #pragma unroll
-    for (int j = XPP * part; j < XPP * (part + 1); ++j)
+    for (int j = (part * XL + 3) / 4; j < ((part + 1) * XL + 3) / 4; ++j)
       load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
   };
   auto frag = [&](int kb, int s, int mb) {
@@ -915,8 +918,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
         for (int cb = 0; cb < CB; ++cb) acc[mb][cb] = mfma32(wf[cur][cb], af[mb], acc[mb][cb]);
         af[mb] = s < 3 ? frag(kb, s + 1, mb) : frag(kb + 1, 0, mb);
       }
-      if (s < 3) interleave_substep<MB * CB, CB, (26 * CB + 15) / 16 + 1>();
-      else interleave_substep<MB * CB, CB, (50 * CB + 15) / 16 + 1>();
+      constexpr int F = MB * CB;  // MFMAs per sub-step
+      if (s < 3) interleave_substep<F, CB, (26 * CB + F - 1) / F + 1>();
+      else interleave_substep<F, CB, (50 * CB + F - 1) / F + 1>();
     }
   };
 
@@ -951,24 +955,28 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
         const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h + t4;
         bv[cb][q][t4] = (bias && n < N) ? bf16_bits_to_f32(bias[n]) : 0.0f;
       }
+  // Every wave is done with the x stages before any wave stages its output
+  // there. The barrier comes before the per-wave choice of store path, so that
+  // every wave of the workgroup reaches it.
+  __syncthreads();
   const bool full_cols = n0 + WN * (wave + 1) <= N;
   if (full_cols && (ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
     // Through LDS, so that every store writes whole 128-byte row segments: a
     // direct store from the MFMA layout writes 16 bytes into each of 32 rows,
     // and each partial line then reaches HBM as a write of its own. Each wave
-    // stages 32*MB/2 rows x WN columns at a time (row stride WN*2+8 bytes: the
-    // 8-byte writes of 32 lanes then hit distinct banks).
-    constexpr int RS = WN * 2 + 8, HALF = MB / 2;
-    static_assert(4 * HALF * 32 * RS <= STAGES * SB, "epilogue staging fits the x stages");
-    __syncthreads();  // every wave is done with the x stages
-    uint8_t *ep = smem + wave * HALF * 32 * RS;
+    // stages HR*32 rows x WN columns at a time (row stride WN*2+8 bytes: the
+    // 8-byte writes of 32 lanes then hit distinct banks), in its own region.
+    constexpr int RS = WN * 2 + 8;
+    constexpr int HR = (NW * (MB / 2) * 32 * RS <= STAGES * SB) ? MB / 2 : 1;
+    static_assert(NW * HR * 32 * RS <= STAGES * SB && MB % HR == 0, "epilogue staging fits the x stages");
+    uint8_t *ep = smem + wave * HR * 32 * RS;
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(Y, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldy * 2,
                                                                              static_cast<int64_t>(0xffffffff))));
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int piece = 0; piece < MB / HR; ++piece) {
 #pragma unroll
-      for (int mh = 0; mh < HALF; ++mh) {
-        const int mb = HALF * half + mh;
+      for (int mh = 0; mh < HR; ++mh) {
+        const int mb = HR * piece + mh;
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
@@ -978,13 +986,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
             *reinterpret_cast<uint2 *>(ep + (32 * mh + c) * RS + 2 * (32 * cb + 8 * q + 4 * h)) = make_uint2(lo, hi);
           }
       }
-      // Row r of the staged block: 8 lanes x 16 bytes; a wave stores 8 rows per instruction.
+      // Row r of the staged block: WN/8 lanes x 16 bytes; a wave stores 512/WN rows per instruction.
+      constexpr int LPR = WN / 8, RPI = 64 / LPR;
 #pragma unroll
-      for (int j = 0; j < HALF * 4; ++j) {
-        const int r = 8 * j + (lane >> 3), col = 8 * (lane & 7);
+      for (int j = 0; j < HR * 32 / RPI; ++j) {
+        const int r = RPI * j + lane / LPR, col = 8 * (lane % LPR);
         const uint8_t *src = ep + r * RS + 2 * col;
         const uint2 v0 = *reinterpret_cast<const uint2 *>(src), v1 = *reinterpret_cast<const uint2 *>(src + 8);
-        const int m = m0 + 32 * HALF * half + r;
+        const int m = m0 + 32 * HR * piece + r;
         // Rows past M fall outside the buffer range and are dropped.
         const uint32_t off = m < M ? static_cast<uint32_t>((static_cast<int64_t>(m) * ldy + n0 + WN * wave + col) * 2)
                                    : 0xffffffffu;
@@ -1018,19 +1027,27 @@ __global__ __launch_bounds__(kGemmThreads, 1) void nf4_gemm_kernel(GemmBatch bat
 }
 
 // `batch.p[0..count)` filled except tiles_n / tile0, which are set here.
-template <int MB, int CB, int STAGES>
+template <int MB, int CB, int STAGES, int NW>
 void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s) {
   int64_t tiles = 0;
   for (int i = 0; i < batch.count; ++i) {
     GemmProblem &p = batch.p[i];
-    const int64_t tiles_m = cdiv(p.M, 32 * MB), tiles_n = cdiv(p.N, 128 * CB);
+    const int64_t tiles_m = cdiv(p.M, 32 * MB), tiles_n = cdiv(p.N, 32 * CB * NW);
     p.tiles_n = static_cast<int>(tiles_n);
     p.tile0 = static_cast<int>(tiles);
     tiles += tiles_m * tiles_n;
   }
   batch.tiles = static_cast<int>(tiles);
   batch.per_xcd = static_cast<int>(cdiv(tiles, 8));
-  nf4_gemm_kernel<MB, CB, STAGES><<<dim3(static_cast<uint32_t>(batch.per_xcd * 8)), dim3(kGemmThreads), 0, s>>>(batch, c);
+  nf4_gemm_kernel<MB, CB, STAGES, NW><<<dim3(static_cast<uint32_t>(batch.per_xcd * 8)), dim3(64 * NW), 0, s>>>(batch, c);
+}
+
+#ifndef SELAS_GEMM_NW
+#define SELAS_GEMM_NW 4
+#endif
+void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s) {
+  if constexpr (SELAS_GEMM_NW == 8) launch_gemm<4, 2, 3, 8>(batch, c, s);
+  else launch_gemm<8, 2, 3, 4>(batch, c, s);
 }
 
 }  // namespace
@@ -1097,7 +1114,7 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
   batch.count = 1;
   batch.p[0] = GemmProblem{xb, packed, absmax, bb, yb, ldx, ldy, static_cast<int>(M), static_cast<int>(K),
                            static_cast<int>(N), 0, 0};
-  launch_gemm<8, 2, 3>(batch, c, s);
+  launch_gemm_default(batch, c, s);
   return check_launch("nf4_linear (gemm)");
 }
 
@@ -1126,7 +1143,7 @@ extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, 
   if (batch.count == 0) return ok();
   Code16 c;
   for (int i = 0; i < 16; ++i) c.v[i] = code[i];
-  launch_gemm<8, 2, 3>(batch, c, static_cast<hipStream_t>(stream));
+  launch_gemm_default(batch, c, static_cast<hipStream_t>(stream));
   return check_launch("nf4_linear_batched");
 }
 

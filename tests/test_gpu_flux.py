@@ -100,3 +100,26 @@ def test_modulations_and_step(model):
     ref = OF.final_layer(g, x[:, 64:], fmod.float(), torch.float32)
     assert out.shape == (1, 64, 64) and torch.isfinite(out).all()
     assert rel(out, ref) < 3e-2
+
+
+def test_batched_step_equals_images_one_by_one(model):
+    # C5 runs batch 4 at 512^2: each image brings its own modulations, and every kernel on the path
+    # works per token (linears, segments) or per (image, head) (attention), so a batched step must
+    # give each image the velocity it gets alone.
+    dev = torch.device("cuda")
+    g = seeded(27)
+    b = 3
+    mods = [model.modulations(torch.nn.functional.silu(torch.randn(4, 1, CFG.hidden, generator=g)).to(torch.bfloat16)
+                              .to(dev)) for _ in range(b)]
+    _, txt, cos, sin = inputs(b, 64, 8)
+    lat = torch.randn(b, 64, 64, generator=g)
+    fmod = (torch.randn(b, 2 * CFG.hidden, generator=g) * 0.3).to(torch.bfloat16)
+    s = 1
+    args = (cos.to(dev), sin.to(dev))
+    out = model.step(lat.to(dev), txt.to(dev), [torch.cat([m[j][s] for m in mods], dim=0) for j in range(len(mods[0]))],
+                     fmod.to(dev), *args)
+    assert out.shape == (b, 64, 64) and torch.isfinite(out).all()
+    for i in range(b):
+        one = model.step(lat[i:i + 1].to(dev), txt[i:i + 1].to(dev), [m[s] for m in mods[i]], fmod[i:i + 1].to(dev),
+                         *args)
+        assert rel(out[i:i + 1], one.cpu()) < 1e-3

@@ -14,9 +14,15 @@ The same JSON line carries:
   extra         the other configurations: the 1536-token single linear, the 76 hoisted
                 modulation GEMMs at M = 28 (HBM-bound, GB/s), the fused segments at M = 4608
                 (GB/s), the library dequant + hipBLASLt path on the GPU for comparison, and
-                with --full-step the full FLUX-dev-shaped step at 1024^2 (s/step).
+                the full FLUX-dev-shaped step (batch 1 at 1024^2 and batch 4 at 512^2; s/step
+                against the lower bound linear FLOP / peak + attention FLOP / peak + segment
+                bytes / HBM peak).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--full-step] [--no-extra] [--no-cpu]
+Per-kernel figures are medians of HIP-event times over the timed steps (the roofline figure uses
+the mean, as a kernel trace's average does). The default 30 warmup steps take the GPU past its
+clock ramp under sustained load.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-full-step] [--no-extra] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -438,7 +444,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=3)
+    # Under sustained GEMM load the GPU takes ~60 launches (~35 ms) to reach its steady clock
+    # (linear1: 985 TFLOP/s in the first 20 launches, 1,155 from the 60th on); 30 untimed steps
+    # (60 launches) get past that ramp.
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-full-step", action="store_true",
                     help="skip the full FLUX-dev-shaped steps (batch 1 at 1024^2, batch 4 at 512^2)")
     ap.add_argument("--no-extra", action="store_true")

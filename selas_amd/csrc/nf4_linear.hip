@@ -956,8 +956,12 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
         bv[cb][q][t4] = (bias && n < N) ? bf16_bits_to_f32(bias[n]) : 0.0f;
       }
   // Every wave is done with the x stages before any wave stages its output
-  // there. The barrier comes before the per-wave choice of store path, so that
-  // every wave of the workgroup reaches it.
+  // there: its own loads into LDS have landed (the last K blocks' look-ahead
+  // DMAs may still be in flight; the workgroup barrier alone does not wait for
+  // them) and the barrier then covers the other waves. It comes before the
+  // per-wave choice of store path, so that every wave of the workgroup reaches
+  // it, and it also leaves no DMA in flight when the workgroup ends.
+  wait_vmcnt<0>();
   __syncthreads();
   const bool full_cols = n0 + WN * (wave + 1) <= N;
   if (full_cols && (ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
@@ -1042,13 +1046,10 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s) {
   nf4_gemm_kernel<MB, CB, STAGES, NW><<<dim3(static_cast<uint32_t>(batch.per_xcd * 8)), dim3(64 * NW), 0, s>>>(batch, c);
 }
 
-#ifndef SELAS_GEMM_NW
-#define SELAS_GEMM_NW 4
-#endif
-void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s) {
-  if constexpr (SELAS_GEMM_NW == 8) launch_gemm<4, 2, 3, 8>(batch, c, s);
-  else launch_gemm<8, 2, 3, 4>(batch, c, s);
-}
+// Every launch uses 256 x 256 tiles of 4 waves (256 x 64 each), 3 LDS stages.
+// 128 x 512 tiles of 8 waves (128 x 64 each, two waves per SIMD) measured 15-25 %
+// slower: each decoded weight fragment then serves 4 MFMAs instead of 8.
+void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s) { launch_gemm<8, 2, 3, 4>(batch, c, s); }
 
 }  // namespace
 }  // namespace selas

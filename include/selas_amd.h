@@ -210,6 +210,30 @@ int selas_gelu(const void *h, int64_t rows, int64_t cols, int64_t ld, void *out,
 int selas_attn_mlp(const void *attn, int64_t rows, int64_t Da, int64_t lda, const void *mlp, int64_t Dm,
                    int64_t ldm, void *out, int dtype, void *stream);
 
+/* ------------------------------------------------------------ attention
+ *
+ * The block attention (selas/models/flux.py:135-138): SDPA over q, k, v
+ * [B, H, L, Dh] followed by transpose(1, 2).reshape(B, L, H*Dh).
+ */
+
+/*
+ * out[b, l, h*Dh + d] = sum_j softmax_j(q[b,h,l,:] . k[b,h,j,:] / sqrt(Dh)) v[b,h,j,d]
+ * with q, k [B, H, L, Dh] contiguous, the values given transposed as vt
+ * [B, H, Dh, L] (selas_transpose_heads), out [B, L, H*Dh] contiguous. bf16 in
+ * and out; scores, softmax and sums in fp32, the probabilities rounded to bf16
+ * for the second product (as the flash backends of torch's SDPA do). Takes
+ * Dh = 128 and L % 128 == 0; otherwise SELAS_EUNSUPPORTED (the caller runs SDPA).
+ * Replaces _attention (flux.py:135-138).
+ */
+int selas_attention(const void *q, const void *k, const void *vt, int64_t B, int64_t H, int64_t L, int64_t Dh,
+                    void *out, int dtype, void *stream);
+
+/*
+ * vt[i, d, l] = v[i, l, d] for BH heads of [L, Dh] (bf16, Dh = 128, L % 128 == 0):
+ * the value layout selas_attention reads. No counterpart in the reference.
+ */
+int selas_transpose_heads(const void *v, int64_t BH, int64_t L, int64_t Dh, void *vt, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

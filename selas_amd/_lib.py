@@ -39,6 +39,8 @@ SIGNATURES: dict[str, list] = {
                          _P, _P, _INT, _P],
     "selas_gelu": [_P, _I64, _I64, _I64, _P, _INT, _P],
     "selas_attn_mlp": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _INT, _P],
+    "selas_attention": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _INT, _P],
+    "selas_transpose_heads": [_P, _I64, _I64, _I64, _P, _INT, _P],
 }
 
 

@@ -1,0 +1,260 @@
+// Fused attention forward of the FLUX blocks (head dim 128, no mask) for gfx950:
+// softmax(q k^T / sqrt(128)) v for every (batch, head), written straight into the
+// [B, L, H * 128] layout the projection linear reads.
+//
+// One workgroup = 4 waves = 128 queries of one (batch, head); wave w owns queries
+// 32w .. 32w+31. The keys stream through LDS in tiles of 64 (K rows and the
+// matching V^T columns, double-buffered, loaded by buffer->LDS DMA). Per tile:
+//   * S^T = K Q^T on 32x32x16 MFMAs (16 per wave): K from LDS is the A operand,
+//     Q (held in registers for the whole loop) the B operand, so lane l holds 32
+//     scores of query l % 32 (lanes l and l^32 together hold its 64 keys);
+//   * online softmax in the exp2 domain: the running maximum is raised only when
+//     a tile's maximum exceeds it by more than 8 (2^8 headroom in fp32 and in the
+//     bf16 probabilities), so the rescale of the output is rare;
+//   * O^T += V^T P^T (16 MFMAs): the probabilities, rounded to bf16, are the B
+//     operand straight from the score registers. For that, the K rows of a 32-key
+//     block are loaded with bits 2 and 3 of the row index swapped: lane (q, h)
+//     register r then holds key 16*(r/8) + 8*h + r%8, i.e. 8 consecutive keys per
+//     MFMA k-step, and the V^T operand reads 8 consecutive keys (16 bytes).
+// LDS tiles are XOR-swizzled in 16-byte chunks so that the fragment reads (16
+// lanes per LDS cycle) hit 16 distinct 4-bank groups.
+#include "common.h"
+
+namespace selas {
+namespace {
+
+constexpr int kDh = 128;                   // head dim
+constexpr int kQT = 128;                   // queries per workgroup (4 waves x 32)
+constexpr int kKT = 64;                    // keys per tile
+constexpr int kTileBytes = kKT * kDh * 2;  // one K tile or V^T tile: 16 KiB
+constexpr int kStageBytes = 2 * kTileBytes;
+
+// MFMA row rho of a 32-key block reads K row swap23(rho): bits 2 and 3 exchanged.
+__device__ __forceinline__ int swap23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const uint16_t *__restrict__ q,
+                                                          const uint16_t *__restrict__ k,
+                                                          const uint16_t *__restrict__ vt, uint16_t *__restrict__ out,
+                                                          int H, int L, int qtiles, int per_xcd, int total,
+                                                          float c2) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
+  // Work item t = (b % 8) * per_xcd + b / 8: each XCD takes a contiguous range,
+  // so the query tiles of one head share that head's K and V^T in its L2.
+  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (t >= total) return;
+  const int bh = t / qtiles, qt = t - bh * qtiles;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c = lane & 31;
+  const int64_t head = static_cast<int64_t>(bh) * L * kDh;  // elements
+  const uint32_t head_bytes = static_cast<uint32_t>(L) * kDh * 2;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + head, head_bytes);
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + head, head_bytes);
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc(vt + head, head_bytes);
+
+  // Q as the B operand of S^T = K Q^T: lane (query c of this wave, h) holds d = 16s + 8h .. +8.
+  const int q_row = qt * kQT + 32 * wave + c;
+  bf16x8 qf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    qf[s] = __builtin_bit_cast(bf16x8, load_b128(qr, static_cast<uint32_t>(q_row) * 256u + (16 * s + 8 * h) * 2, 0));
+
+  // DMA per tile: 16 instructions of 1 KiB for K (4 rows of 256 B each) and 16
+  // for V^T (8 rows of 128 B), 4 + 4 per wave. Lane i of K instruction J fills
+  // row r = 4J + i/16, physical chunk i%16, with logical chunk (i%16) ^ (r%16);
+  // lane i of V^T instruction J fills row d = 8J + i/8, physical chunk i%8, with
+  // logical chunk (i%8) ^ ((d/2)%8). The tile's first key goes in the scalar offset.
+  uint32_t k_voff[4], v_voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int J = 4 * wave + j;
+    const int r = 4 * J + (lane >> 4);
+    k_voff[j] = static_cast<uint32_t>(r) * 256u + ((static_cast<uint32_t>(lane & 15) ^ (r & 15)) << 4);
+    const int d = 8 * J + (lane >> 3);
+    v_voff[j] = static_cast<uint32_t>(d) * static_cast<uint32_t>(L) * 2u +
+                ((static_cast<uint32_t>(lane & 7) ^ ((d >> 1) & 7)) << 4);
+  }
+  auto issue = [&](int stage, int kt) {
+    uint8_t *base = smem + stage * kStageBytes;
+    const uint32_t key0 = static_cast<uint32_t>(kt) * kKT;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_lds16(kr, base + (4 * wave + j) * 1024, k_voff[j], key0 * 256u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_lds16(vr, base + kTileBytes + (4 * wave + j) * 1024, v_voff[j], key0 * 2u);
+  };
+  // A-operand fragments: K row of MFMA row c in key block kb, d-chunk 2s+h; V^T
+  // row d = 32db + c, key chunk 4kb + 2t + h (keys 32kb + 16t + 8h .. +8).
+  const int krow = swap23(c);
+  auto kfrag = [&](int stage, int kb, int s) {
+    const int r = 32 * kb + krow;
+    const int cc = 2 * s + h;
+    return *reinterpret_cast<const bf16x8 *>(smem + stage * kStageBytes + r * 256 + ((cc ^ (r & 15)) << 4));
+  };
+  auto vfrag = [&](int stage, int db, int kb, int t2) {
+    const int d = 32 * db + c;
+    const int cc = 4 * kb + 2 * t2 + h;
+    return *reinterpret_cast<const bf16x8 *>(smem + stage * kStageBytes + kTileBytes + d * 128 +
+                                             ((cc ^ ((d >> 1) & 7)) << 4));
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  const int ntiles = L / kKT;
+
+  issue(0, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  auto tile = [&](int stage, int kt) {
+    if (kt + 1 < ntiles) issue(stage ^ 1, kt + 1);
+    f32x16 sc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc[kb] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sc[kb] = mfma32(kfrag(stage, kb, s), qf[s], sc[kb]);
+    }
+    float mx = sc[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
+    mx = fmaxf(mx, xor32(mx)) * c2;
+    if (mx > m_run + 8.0f) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mx);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+      l_run *= alpha;
+      m_run = mx;
+    }
+    float ls = 0.0f;
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * t2 + 2 * e], c2, -m_run));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * t2 + 2 * e + 1], c2, -m_run));
+          ls += p0 + p1;
+          w[e] = pack_bf16x2(p0, p1);
+        }
+        pb[kb][t2] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+      }
+    l_run += ls;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) o[db] = mfma32(vfrag(stage, db, kb, t2), pb[kb][t2], o[db]);
+    // The next tile has landed for this wave; the barrier then covers every wave
+    // and orders this tile's LDS reads before the DMA that reuses its stage.
+    wait_vmcnt<0>();
+    __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 2 <= ntiles; kt += 2) {
+    tile(0, kt);
+    tile(1, kt + 1);
+  }
+  if (kt < ntiles) tile(0, kt);
+
+  // out[b, q, hh*128 + d] = O^T[d][q] / l, d = 32db + 8g + 4h + e for register 4g + e.
+  const float inv = 1.0f / (l_run + xor32(l_run));
+  const int b = bh / H, hh = bh - b * H;
+  uint16_t *orow = out + (static_cast<int64_t>(b) * L + q_row) * (static_cast<int64_t>(H) * kDh) + hh * kDh;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * h;
+      *reinterpret_cast<uint2 *>(orow + d) = make_uint2(pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
+                                                        pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
+    }
+}
+
+// vt[bh][d][l] = v[bh][l][d] for 64 tokens x 128 channels per workgroup, through LDS.
+__global__ __launch_bounds__(256) void transpose_heads_kernel(const uint16_t *__restrict__ v, uint16_t *__restrict__ vt,
+                                                              int L) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kDh][kKT + 8];  // row stride 144 B
+  const int l0 = blockIdx.x * kKT;
+  const int64_t head = static_cast<int64_t>(blockIdx.y) * L * kDh;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // token r, channels 8c .. 8c+7
+    const int r = (tid >> 4) + 16 * i, ch = tid & 15;
+    const uint4 x = *reinterpret_cast<const uint4 *>(v + head + static_cast<int64_t>(l0 + r) * kDh + 8 * ch);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[8 * ch + 2 * e][r] = static_cast<uint16_t>(w[e]);
+      tile[8 * ch + 2 * e + 1][r] = static_cast<uint16_t>(w[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // channel d, tokens 8c .. 8c+7
+    const int d = (tid >> 3) + 32 * i, ch = tid & 7;
+    *reinterpret_cast<uint4 *>(vt + head + static_cast<int64_t>(d) * L + l0 + 8 * ch) =
+        *reinterpret_cast<const uint4 *>(&tile[d][8 * ch]);
+  }
+}
+
+}  // namespace
+}  // namespace selas
+
+using namespace selas;
+
+namespace {
+int check_heads(const char *what, int64_t B, int64_t H, int64_t L, int64_t Dh, int dtype) {
+  if (B < 0 || H < 0 || L < 0 || Dh <= 0)
+    return set_error(SELAS_EINVAL, "%s: bad shape B=%lld H=%lld L=%lld Dh=%lld", what, (long long)B, (long long)H,
+                     (long long)L, (long long)Dh);
+  if (!valid_dtype(dtype)) return set_error(SELAS_EINVAL, "%s: bad dtype %d", what, dtype);
+  if (dtype != SELAS_BF16 || Dh != kDh || L % kQT)
+    return set_error(SELAS_EUNSUPPORTED, "%s: fused attention takes bf16, head_dim 128 and L %% 128 == 0 "
+                                         "(got %s, %lld, %lld)", what, dtype_name(dtype), (long long)Dh, (long long)L);
+  if (L * Dh * 2 >= (1ll << 32) || B * H >= (1ll << 31) / 64)
+    return set_error(SELAS_EUNSUPPORTED, "%s: a head above 4 GiB", what);
+  return SELAS_OK;
+}
+}  // namespace
+
+extern "C" int selas_attention(const void *q, const void *k, const void *vt, int64_t B, int64_t H, int64_t L,
+                               int64_t Dh, void *out, int dtype, void *stream) {
+  if (int e = check_heads("attention", B, H, L, Dh, dtype)) return e;
+  if (B == 0 || H == 0 || L == 0) return ok();
+  if (!q || !k || !vt || !out) return set_error(SELAS_EINVAL, "attention: null pointer");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(vt, 16) || !aligned(out, 8))
+    return set_error(SELAS_EUNSUPPORTED, "attention: q, k, v^T must be 16-byte aligned, out 8-byte aligned");
+  const int qtiles = static_cast<int>(L / kQT);
+  const int64_t total = B * H * qtiles;
+  const int per_xcd = static_cast<int>(cdiv(total, 8));
+  const float c2 = 1.4426950408889634f / sqrtf(static_cast<float>(Dh));  // log2(e) / sqrt(Dh)
+  attn_fwd_kernel<<<dim3(static_cast<uint32_t>(per_xcd * 8)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(vt),
+      static_cast<uint16_t *>(out), static_cast<int>(H), static_cast<int>(L), qtiles, per_xcd, static_cast<int>(total),
+      c2);
+  return check_launch("attention");
+}
+
+extern "C" int selas_transpose_heads(const void *v, int64_t BH, int64_t L, int64_t Dh, void *vt, int dtype,
+                                     void *stream) {
+  if (int e = check_heads("transpose_heads", 1, BH, L, Dh, dtype)) return e;
+  if (BH == 0 || L == 0) return ok();
+  if (!v || !vt) return set_error(SELAS_EINVAL, "transpose_heads: null pointer");
+  if (!aligned(v, 16) || !aligned(vt, 16))
+    return set_error(SELAS_EUNSUPPORTED, "transpose_heads: v and v^T must be 16-byte aligned");
+  if (BH > 65535) return set_error(SELAS_EUNSUPPORTED, "transpose_heads: more than 65535 heads");
+  transpose_heads_kernel<<<dim3(static_cast<uint32_t>(L / kKT), static_cast<uint32_t>(BH)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t *>(v),
+                                                               static_cast<uint16_t *>(vt), static_cast<int>(L));
+  return check_launch("transpose_heads");
+}

@@ -64,14 +64,27 @@ def image_ids(h: int, w: int, device=None) -> torch.Tensor:
     return ids.reshape(h * w, 3)
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-    """SDPA over [B, H, L, Dh] -> [B, L, H*Dh] on the fused backends only."""
+def sdpa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """The reference's attention (flux.py:135-138): SDPA over [B, H, L, Dh] -> [B, L, H*Dh], on torch's
+    fused backends only."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     b, h, l, d = q.shape
     with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
         out = F.scaled_dot_product_attention(q, k, v)
     return out.transpose(1, 2).reshape(b, l, h * d)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """[B, H, L, Dh] -> [B, L, H*Dh]: the fused gfx950 kernel (selas_amd.attention), or SDPA for the
+    shapes it does not take (head dim other than 128, L not a multiple of 128)."""
+    from . import _lib
+    from .attention import attention as fused_attention
+
+    try:
+        return fused_attention(q, k, v)
+    except _lib.Unsupported:
+        return sdpa_attention(q, k, v)
 
 
 def _linear_pair(w, a, b):

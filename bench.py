@@ -13,7 +13,8 @@ The same JSON line carries:
                 F.linear in fp32) on the host cores, on a bounded row sample;
   extra         the other configurations: the 1536-token single linear, the 76 hoisted
                 modulation GEMMs at M = 28 (HBM-bound, GB/s), the fused segments at M = 4608
-                (GB/s), the library dequant + hipBLASLt path on the GPU for comparison, and
+                (GB/s), the library dequant + hipBLASLt path on the GPU for comparison, the fused
+                attention against torch's SDPA at the FLUX shapes, and
                 the full FLUX-dev-shaped step (batch 1 at 1024^2 and batch 4 at 512^2; s/step
                 against the lower bound linear FLOP / peak + attention FLOP / peak + segment
                 bytes / HBM peak).
@@ -310,6 +311,44 @@ def segment_bytes(kind: str, cfg, l_img: int, l_txt: int, batch: int) -> float:
     return 0.0
 
 
+def bench_attention(dev, steps, warmup):
+    """The block attention at 1024^2 (B = 1, 24 heads x 128, L = 4608) and at 512^2 with batch 4 (L = 1536):
+    the fused kernel (its launch alone, and the call with the value transpose) against the reference's
+    SDPA + transpose/reshape (torch's flash backends)."""
+    from selas_amd import _lib
+    from selas_amd import flux as F
+    from selas_amd.attention import attention, transpose_heads
+
+    out = {}
+    for name, b, l in (("b1_1024", 1, 4608), ("b4_512", 4, 1536)):
+        g = torch.Generator(device=dev).manual_seed(6)
+        q, k, v = (torch.randn(b, 24, l, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+        vt = transpose_heads(v)
+        o = torch.empty(b, l, 24 * 128, dtype=torch.bfloat16, device=dev)
+
+        def kernel():
+            _lib.call("selas_attention", q.data_ptr(), k.data_ptr(), vt.data_ptr(), b, 24, l, 128, o.data_ptr(),
+                      _lib.BF16, _lib.stream(dev))
+
+        runs = {"kernel": kernel, "fused_call": lambda: attention(q, k, v), "sdpa": lambda: F.sdpa_attention(q, k, v)}
+        flop = 4.0 * b * 24 * l * l * 128
+        res = {"shape": [b, 24, l, 128], "flop": flop}
+        for key, fn in runs.items():
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize(dev)
+            tm = Timer()
+            for _ in range(steps):
+                t = tm.start(key)
+                fn()
+                tm.stop(t)
+            torch.cuda.synchronize(dev)
+            ms = tm.median_ms(key)
+            res[key] = {"ms": ms, "tflops": flop / ms / 1e9}
+        out[name] = res
+    return out
+
+
 def bench_full_step(dev, steps, warmup, batch=1, res=1024):
     """FLUX-dev-shaped step (19 double + 38 single blocks, all NF4 weights resident) at res^2 with
     `batch` images. Each image's 28-step modulations come from its own grouped skinny launch (outside
@@ -476,6 +515,9 @@ def main():
         log(f"bench: segments {json.dumps({k: round(v['gbs']) for k, v in extra['segments_m4608'].items()})}")
         extra["library_path"] = bench_library_path(dev, a.steps, a.warmup)
         log(f"bench: library path {extra['library_path']['tflops']:.1f} TFLOP/s")
+        extra["attention"] = bench_attention(dev, a.steps, a.warmup)
+        log("bench: attention " + ", ".join(f"{k}: fused {v['kernel']['tflops']:.0f} / SDPA {v['sdpa']['tflops']:.0f} TFLOP/s"
+                                            for k, v in extra["attention"].items()))
     if not a.no_full_step:
         fs_steps = max(3, a.steps // 5)
         for key, batch, res_px in (("full_step_1024_b1", 1, 1024), ("full_step_512_b4", 4, 512)):

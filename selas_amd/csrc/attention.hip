@@ -18,6 +18,11 @@
 //     MFMA k-step, and the V^T operand reads 8 consecutive keys (16 bytes).
 // LDS tiles are XOR-swizzled in 16-byte chunks so that the fragment reads (16
 // lanes per LDS cycle) hit 16 distinct 4-bank groups.
+//
+// LDS bandwidth bounds this kernel: every MFMA reads a 1 KiB A fragment from LDS
+// (halving those reads ran 24 % faster). Two query blocks per wave would share
+// each fragment, but need about 500 registers (one wave per SIMD); that version
+// ran 25 % slower, because a lone wave cannot overlap its softmax with MFMAs.
 #include "common.h"
 
 namespace selas {
@@ -32,7 +37,17 @@ constexpr int kStageBytes = 2 * kTileBytes;
 // MFMA row rho of a 32-key block reads K row swap23(rho): bits 2 and 3 exchanged.
 __device__ __forceinline__ int swap23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
-__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+// max / sum of v over lanes l and l ^ 32 (the two halves of one query's keys), by
+// v_permlane32_swap: its first result holds lanes 0-31's v in every lane, the
+// second lanes 32-63's.
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const uint16_t *__restrict__ q,
                                                           const uint16_t *__restrict__ k,
@@ -123,7 +138,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const uint16_t *__rest
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
-    mx = fmaxf(mx, xor32(mx)) * c2;
+    mx = pair_max(mx) * c2;
     if (mx > m_run + 8.0f) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - mx);
 #pragma unroll
@@ -167,7 +182,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const uint16_t *__rest
   if (kt < ntiles) tile(0, kt);
 
   // out[b, q, hh*128 + d] = O^T[d][q] / l, d = 32db + 8g + 4h + e for register 4g + e.
-  const float inv = 1.0f / (l_run + xor32(l_run));
+  const float inv = 1.0f / pair_sum(l_run);
   const int b = bh / H, hh = bh - b * H;
   uint16_t *orow = out + (static_cast<int64_t>(b) * L + q_row) * (static_cast<int64_t>(H) * kDh) + hh * kDh;
 #pragma unroll

@@ -328,7 +328,7 @@ def bench_attention(dev, steps, warmup):
 
         def kernel():
             _lib.call("selas_attention", q.data_ptr(), k.data_ptr(), vt.data_ptr(), b, 24, l, 128, o.data_ptr(),
-                      _lib.BF16, _lib.stream(dev))
+                      24 * 128, _lib.BF16, _lib.stream(dev))
 
         runs = {"kernel": kernel, "fused_call": lambda: attention(q, k, v), "sdpa": lambda: F.sdpa_attention(q, k, v)}
         flop = 4.0 * b * 24 * l * l * 128

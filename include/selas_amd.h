@@ -100,7 +100,13 @@ int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uin
 #define SELAS_MAX_BATCHED_LINEARS 4
 
 /* One quantized linear of a batched launch (host-memory array element); the
- * fields mean what the arguments of selas_nf4_linear mean. */
+ * first fields mean what the arguments of selas_nf4_linear mean.
+ * gelu_cols (0 = none) makes the last gelu_cols output columns
+ * y2[m, j] = bf16(gelu_tanh(bf16(x W^T + b)[m, N - gelu_cols + j])) instead, with
+ * row stride ldy2: the GELU that follows the block's MLP input linears
+ * (flux.py:194-200), applied to the rounded output exactly as a separate GELU
+ * kernel would. N - gelu_cols must be a multiple of 256; with gelu_cols = N, y
+ * is not written and may be NULL. */
 typedef struct selas_nf4_gemm_problem {
   const void *x;
   int64_t M, K, ldx;
@@ -110,6 +116,8 @@ typedef struct selas_nf4_gemm_problem {
   const void *bias;
   void *y;
   int64_t ldy;
+  void *y2;
+  int64_t ldy2, gelu_cols;
 } selas_nf4_gemm_problem;
 
 /*
@@ -219,14 +227,16 @@ int selas_attn_mlp(const void *attn, int64_t rows, int64_t Da, int64_t lda, cons
 /*
  * out[b, l, h*Dh + d] = sum_j softmax_j(q[b,h,l,:] . k[b,h,j,:] / sqrt(Dh)) v[b,h,j,d]
  * with q, k [B, H, L, Dh] contiguous, the values given transposed as vt
- * [B, H, Dh, L] (selas_transpose_heads), out [B, L, H*Dh] contiguous. bf16 in
+ * [B, H, Dh, L] (selas_transpose_heads), out [B, L, H*Dh] with row stride ldo
+ * (>= H*Dh; e.g. the first columns of the [attention | GELU(mlp)] input of the
+ * single block's second linear, flux.py:198-200). bf16 in
  * and out; scores, softmax and sums in fp32, the probabilities rounded to bf16
  * for the second product (as the flash backends of torch's SDPA do). Takes
  * Dh = 128 and L % 128 == 0; otherwise SELAS_EUNSUPPORTED (the caller runs SDPA).
  * Replaces _attention (flux.py:135-138).
  */
 int selas_attention(const void *q, const void *k, const void *vt, int64_t B, int64_t H, int64_t L, int64_t Dh,
-                    void *out, int dtype, void *stream);
+                    void *out, int64_t ldo, int dtype, void *stream);
 
 /*
  * vt[i, d, l] = v[i, l, d] for BH heads of [L, Dh] (bf16, Dh = 128, L % 128 == 0):

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libselas_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
@@ -39,7 +39,7 @@ SIGNATURES: dict[str, list] = {
                          _P, _P, _INT, _P],
     "selas_gelu": [_P, _I64, _I64, _I64, _P, _INT, _P],
     "selas_attn_mlp": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _INT, _P],
-    "selas_attention": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _INT, _P],
+    "selas_attention": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _INT, _P],
     "selas_transpose_heads": [_P, _I64, _I64, _I64, _P, _INT, _P],
 }
 
@@ -51,7 +51,7 @@ class GemmProblem(ctypes.Structure):
     """selas_nf4_gemm_problem (include/selas_amd.h)."""
 
     _fields_ = [("x", _P), ("M", _I64), ("K", _I64), ("ldx", _I64), ("packed", _P), ("absmax", _P), ("N", _I64),
-                ("bias", _P), ("y", _P), ("ldy", _I64)]
+                ("bias", _P), ("y", _P), ("ldy", _I64), ("y2", _P), ("ldy2", _I64), ("gelu_cols", _I64)]
 
 
 class Unsupported(NotImplementedError):

@@ -36,8 +36,11 @@ def transpose_heads(v: torch.Tensor) -> torch.Tensor:
     return vt
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-    """softmax(q k^T / sqrt(Dh)) v over [B, H, L, Dh] -> [B, L, H * Dh]."""
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(q k^T / sqrt(Dh)) v over [B, H, L, Dh] -> [B, L, H * Dh].
+
+    ``out``: optional [B, L, H * Dh] destination whose rows may be strided (e.g. the first
+    H * Dh columns of a wider buffer); it is returned."""
     q, k = _heads(q, "attention"), _heads(k, "attention")
     if q.shape != k.shape or q.shape != v.shape or q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError(f"attention: q {tuple(q.shape)} {q.dtype}, k {tuple(k.shape)} {k.dtype}, "
@@ -49,9 +52,14 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor
     if d != 128 or l % 128 or q.dtype != torch.bfloat16:
         raise _lib.Unsupported(f"attention: fused kernel takes bf16, head_dim 128 and L % 128 == 0 "
                                f"(got {q.dtype}, {d}, {l})")
+    if out is None:
+        out = torch.empty(b, l, h * d, dtype=q.dtype, device=dev)
+    elif (out.shape != (b, l, h * d) or out.dtype != q.dtype or out.device != q.device or out.stride(-1) != 1
+          or out.stride(0) != l * out.stride(1)):
+        raise ValueError(f"attention: out must be [{b}, {l}, {h * d}] {q.dtype} on {q.device} with unit column "
+                         f"stride and equally spaced rows, got {tuple(out.shape)} strides {out.stride()}")
     vt = transpose_heads(v)
-    out = torch.empty(b, l, h * d, dtype=q.dtype, device=dev)
     with torch.cuda.device(dev):
         _lib.call("selas_attention", q.data_ptr(), k.data_ptr(), vt.data_ptr(), b, h, l, d, out.data_ptr(),
-                  _lib.dtype_code(q.dtype), _lib.stream(dev))
+                  out.stride(1), _lib.dtype_code(q.dtype), _lib.stream(dev))
     return out

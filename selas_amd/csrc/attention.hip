@@ -52,8 +52,8 @@ __device__ __forceinline__ float pair_sum(float v) {
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const uint16_t *__restrict__ q,
                                                           const uint16_t *__restrict__ k,
                                                           const uint16_t *__restrict__ vt, uint16_t *__restrict__ out,
-                                                          int H, int L, int qtiles, int per_xcd, int total,
-                                                          float c2) {
+                                                          int64_t ldo, int H, int L, int qtiles, int per_xcd,
+                                                          int total, float c2) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
   // Work item t = (b % 8) * per_xcd + b / 8: each XCD takes a contiguous range,
   // so the query tiles of one head share that head's K and V^T in its L2.
@@ -181,10 +181,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const uint16_t *__rest
   }
   if (kt < ntiles) tile(0, kt);
 
-  // out[b, q, hh*128 + d] = O^T[d][q] / l, d = 32db + 8g + 4h + e for register 4g + e.
+  // out[(b*L + q) * ldo + hh*128 + d] = O^T[d][q] / l, d = 32db + 8g + 4h + e for register 4g + e.
   const float inv = 1.0f / pair_sum(l_run);
   const int b = bh / H, hh = bh - b * H;
-  uint16_t *orow = out + (static_cast<int64_t>(b) * L + q_row) * (static_cast<int64_t>(H) * kDh) + hh * kDh;
+  uint16_t *orow = out + (static_cast<int64_t>(b) * L + q_row) * ldo + hh * kDh;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -243,20 +243,21 @@ int check_heads(const char *what, int64_t B, int64_t H, int64_t L, int64_t Dh, i
 }  // namespace
 
 extern "C" int selas_attention(const void *q, const void *k, const void *vt, int64_t B, int64_t H, int64_t L,
-                               int64_t Dh, void *out, int dtype, void *stream) {
+                               int64_t Dh, void *out, int64_t ldo, int dtype, void *stream) {
   if (int e = check_heads("attention", B, H, L, Dh, dtype)) return e;
   if (B == 0 || H == 0 || L == 0) return ok();
   if (!q || !k || !vt || !out) return set_error(SELAS_EINVAL, "attention: null pointer");
-  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(vt, 16) || !aligned(out, 8))
-    return set_error(SELAS_EUNSUPPORTED, "attention: q, k, v^T must be 16-byte aligned, out 8-byte aligned");
+  if (ldo < H * Dh) return set_error(SELAS_EINVAL, "attention: out row stride %lld below H*Dh", (long long)ldo);
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(vt, 16) || !aligned(out, 8) || ldo % 4)
+    return set_error(SELAS_EUNSUPPORTED, "attention: q, k, v^T must be 16-byte aligned, out rows 8-byte aligned");
   const int qtiles = static_cast<int>(L / kQT);
   const int64_t total = B * H * qtiles;
   const int per_xcd = static_cast<int>(cdiv(total, 8));
   const float c2 = 1.4426950408889634f / sqrtf(static_cast<float>(Dh));  // log2(e) / sqrt(Dh)
   attn_fwd_kernel<<<dim3(static_cast<uint32_t>(per_xcd * 8)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(vt),
-      static_cast<uint16_t *>(out), static_cast<int>(H), static_cast<int>(L), qtiles, per_xcd, static_cast<int>(total),
-      c2);
+      static_cast<uint16_t *>(out), ldo, static_cast<int>(H), static_cast<int>(L), qtiles, per_xcd,
+      static_cast<int>(total), c2);
   return check_launch("attention");
 }
 

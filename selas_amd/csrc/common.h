@@ -74,6 +74,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// GELU with the tanh approximation, x * 0.5 * (1 + tanh(z)), z = sqrt(2/pi) *
+// (x + 0.044715 x^3), through 0.5 * (1 + tanh(z)) = 1 / (1 + exp(-2z)): one
+// hardware exponential and one reciprocal instead of tanhf (a few ulp of fp32,
+// below the rounding to a 16-bit output). One definition serves the segment
+// kernels and the GEMM epilogue, so both give the same bits.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float kKappa = 0.044715f;
+  const float z = kBeta * (x + kKappa * x * x * x);
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * z));
+}
+
 // fp32 -> bf16 bits, round to nearest even (the rounding torch uses for
 // bfloat16 casts). Any NaN becomes the quiet NaN 0x7FC0.
 __device__ __forceinline__ uint16_t bf16_bits_rne(float f) {

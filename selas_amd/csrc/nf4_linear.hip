@@ -695,14 +695,17 @@ __device__ __forceinline__ void interleave_substep() {
 //     workgroup synchronises; sub-step 3 then overlaps with building the
 //     product tables and first fragments of block kb+1.
 // One problem of a batched launch; its tiles are global tiles [tile0, tile0 + tiles_m * tiles_n).
+// Output columns [n_split, N) are written as bf16(gelu_tanh(bf16(acc + bias)))
+// to Y2 at column n - n_split (row stride ldy2); n_split is N (no such columns)
+// or a multiple of the 256-column tile, so that a tile lies on one side.
 struct GemmProblem {
   const uint16_t *X;
   const uint8_t *packed;
   const float *absmax;
   const uint16_t *bias;
-  uint16_t *Y;
-  int64_t ldx, ldy;
-  int M, K, N, tiles_n, tile0;
+  uint16_t *Y, *Y2;
+  int64_t ldx, ldy, ldy2;
+  int M, K, N, n_split, tiles_n, tile0;
 };
 constexpr int kGemmMaxProblems = 4;
 struct GemmBatch {
@@ -923,6 +926,21 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
         const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h + t4;
         bv[cb][q][t4] = (bias && n < N) ? bf16_bits_to_f32(bias[n]) : 0.0f;
       }
+  // A tile past n_split holds GELU columns (uniform over the workgroup): the sum
+  // is rounded to bf16 as it would be stored, GELU'd in fp32 and rounded again,
+  // exactly what a separate GELU kernel reading the stored output computes.
+  const bool gelu = n0 >= P.n_split;
+  uint16_t *const Yo = gelu ? P.Y2 : Y;
+  const int64_t ldo = gelu ? P.ldy2 : ldy;
+  const int cs = gelu ? P.n_split : 0;  // column shift into Yo
+  auto gelu1 = [](float v) {
+    const __bf16 r = static_cast<__bf16>(materialize(v));
+    return bf16_bits_rne(gelu_tanh_fast(static_cast<float>(r)));
+  };
+  auto out2 = [&](float a, float b) -> uint32_t {
+    if (gelu) return gelu1(a) | (static_cast<uint32_t>(gelu1(b)) << 16);
+    return pack_bf16x2(a, b);
+  };
   // Every wave is done with the x stages before any wave stages its output
   // there: its own loads into LDS have landed (the last K blocks' look-ahead
   // DMAs may still be in flight; the workgroup barrier alone does not wait for
@@ -932,7 +950,7 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
   wait_vmcnt<0>();
   __syncthreads();
   const bool full_cols = n0 + WN * (wave + 1) <= N;
-  if (full_cols && (ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+  if (full_cols && (ldo & 7) == 0 && (reinterpret_cast<uintptr_t>(Yo) & 15) == 0) {
     // Through LDS, so that every store writes whole 128-byte row segments: a
     // direct store from the MFMA layout writes 16 bytes into each of 32 rows,
     // and each partial line then reaches HBM as a write of its own. Each wave
@@ -942,8 +960,8 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
     constexpr int HR = (NW * (MB / 2) * 32 * RS <= STAGES * SB) ? MB / 2 : 1;
     static_assert(NW * HR * 32 * RS <= STAGES * SB && MB % HR == 0, "epilogue staging fits the x stages");
     uint8_t *ep = smem + wave * HR * 32 * RS;
-    const __amdgpu_buffer_rsrc_t yr = make_rsrc(Y, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldy * 2,
-                                                                             static_cast<int64_t>(0xffffffff))));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(Yo, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldo * 2,
+                                                                              static_cast<int64_t>(0xffffffff))));
 #pragma unroll
     for (int piece = 0; piece < MB / HR; ++piece) {
 #pragma unroll
@@ -953,8 +971,8 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
         for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = pack_bf16x2(acc[mb][cb][4 * q] + bv[cb][q][0], acc[mb][cb][4 * q + 1] + bv[cb][q][1]);
-            const uint32_t hi = pack_bf16x2(acc[mb][cb][4 * q + 2] + bv[cb][q][2], acc[mb][cb][4 * q + 3] + bv[cb][q][3]);
+            const uint32_t lo = out2(acc[mb][cb][4 * q] + bv[cb][q][0], acc[mb][cb][4 * q + 1] + bv[cb][q][1]);
+            const uint32_t hi = out2(acc[mb][cb][4 * q + 2] + bv[cb][q][2], acc[mb][cb][4 * q + 3] + bv[cb][q][3]);
             *reinterpret_cast<uint2 *>(ep + (32 * mh + c) * RS + 2 * (32 * cb + 8 * q + 4 * h)) = make_uint2(lo, hi);
           }
       }
@@ -967,8 +985,8 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
         const uint2 v0 = *reinterpret_cast<const uint2 *>(src), v1 = *reinterpret_cast<const uint2 *>(src + 8);
         const int m = m0 + 32 * HR * piece + r;
         // Rows past M fall outside the buffer range and are dropped.
-        const uint32_t off = m < M ? static_cast<uint32_t>((static_cast<int64_t>(m) * ldy + n0 + WN * wave + col) * 2)
-                                   : 0xffffffffu;
+        const uint32_t off =
+            m < M ? static_cast<uint32_t>((static_cast<int64_t>(m) * ldo + n0 - cs + WN * wave + col) * 2) : 0xffffffffu;
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{v0.x, v0.y, v1.x, v1.y}, yr, off, 0, 0);
       }
@@ -984,14 +1002,15 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
       for (int mb = 0; mb < MB; ++mb) {
         const int m = m0 + 32 * mb + c;
         if (m >= M) continue;
-        uint16_t *dst = Y + static_cast<int64_t>(m) * ldy + n;
+        uint16_t *dst = Yo + static_cast<int64_t>(m) * ldo + (n - cs);
         const float v0 = acc[mb][cb][4 * q] + bv[cb][q][0], v1 = acc[mb][cb][4 * q + 1] + bv[cb][q][1];
         const float v2 = acc[mb][cb][4 * q + 2] + bv[cb][q][2], v3 = acc[mb][cb][4 * q + 3] + bv[cb][q][3];
         if (n + 3 < N) {
-          *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+          *reinterpret_cast<uint2 *>(dst) = make_uint2(out2(v0, v1), out2(v2, v3));
         } else {
           const float v[4] = {v0, v1, v2, v3};
-          for (int t4 = 0; t4 < 4 && n + t4 < N; ++t4) dst[t4] = bf16_bits_rne(v[t4]);
+          for (int t4 = 0; t4 < 4 && n + t4 < N; ++t4)
+            dst[t4] = gelu ? gelu1(v[t4]) : bf16_bits_rne(v[t4]);
         }
       }
     }
@@ -1081,8 +1100,8 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
   }
   GemmBatch batch{};
   batch.count = 1;
-  batch.p[0] = GemmProblem{xb, packed, absmax, bb, yb, ldx, ldy, static_cast<int>(M), static_cast<int>(K),
-                           static_cast<int>(N), 0, 0};
+  batch.p[0] = GemmProblem{xb, packed, absmax, bb, yb, nullptr, ldx, ldy, 0, static_cast<int>(M),
+                           static_cast<int>(K), static_cast<int>(N), static_cast<int>(N), 0, 0};
   launch_gemm_default(batch, c, s);
   return check_launch("nf4_linear (gemm)");
 }
@@ -1090,30 +1109,47 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
 extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
                                         const float code[16], int dtype, void *stream) {
   static_assert(kGemmMaxProblems == SELAS_MAX_BATCHED_LINEARS, "batch size");
+  const char *what = "nf4_linear_batched";
   if (count < 0 || count > kGemmMaxProblems)
-    return set_error(SELAS_EINVAL, "nf4_linear_batched: count %lld outside [0, %d]", (long long)count,
-                     kGemmMaxProblems);
-  if (count > 0 && !problems) return set_error(SELAS_EINVAL, "nf4_linear_batched: null problems");
+    return set_error(SELAS_EINVAL, "%s: count %lld outside [0, %d]", what, (long long)count, kGemmMaxProblems);
+  if (count > 0 && !problems) return set_error(SELAS_EINVAL, "%s: null problems", what);
   GemmBatch batch{};
   for (int64_t i = 0; i < count; ++i) {
     const selas_nf4_gemm_problem &q = problems[i];
-    if (int e = check_linear("nf4_linear_batched", q.x, q.M, q.K, q.ldx, q.packed, q.absmax, blocksize, code, q.N,
-                             q.bias, q.y, q.ldy, dtype))
+    const int64_t gc = q.gelu_cols;
+    if (gc < 0 || gc > q.N)
+      return set_error(SELAS_EINVAL, "%s: gelu_cols %lld outside [0, N=%lld]", what, (long long)gc, (long long)q.N);
+    // y holds the first N - gelu_cols columns (row stride ldy >= that); with
+    // every column GELU'd into y2 it is not written and may be NULL.
+    const void *y = (gc == q.N && gc > 0 && !q.y) ? q.y2 : q.y;
+    const int64_t ldy_chk = gc > 0 ? std::max<int64_t>(q.ldy, q.N) : q.ldy;
+    if (int e = check_linear(what, q.x, q.M, q.K, q.ldx, q.packed, q.absmax, blocksize, code, q.N, q.bias, y, ldy_chk,
+                             dtype))
       return e;
+    if (gc > 0 && gc < q.N && q.ldy < q.N - gc)
+      return set_error(SELAS_EINVAL, "%s: ldy %lld below the %lld plain columns", what, (long long)q.ldy,
+                       (long long)(q.N - gc));
+    if (gc > 0) {
+      if (!q.y2 || q.ldy2 < gc) return set_error(SELAS_EINVAL, "%s: gelu_cols needs y2 with ldy2 >= gelu_cols", what);
+      if ((q.N - gc) % (32 * 2 * 4) || (gc < q.N && q.ldy % 4) || !aligned(q.y2, 8) || q.ldy2 % 4 ||
+          q.M * q.ldy2 * 2 >= (1ll << 32))
+        return set_error(SELAS_EUNSUPPORTED, "%s: the GELU columns must start at a multiple of 256, y and y2 "
+                                             "rows 8-byte aligned and y2 below 4 GiB", what);
+    }
     if (q.M == 0) continue;
     if (q.M <= 32)
-      return set_error(SELAS_EUNSUPPORTED, "nf4_linear_batched: M <= 32 runs the skinny kernel (M=%lld)",
-                       (long long)q.M);
+      return set_error(SELAS_EUNSUPPORTED, "%s: M <= 32 runs the skinny kernel (M=%lld)", what, (long long)q.M);
     batch.p[batch.count++] = GemmProblem{static_cast<const uint16_t *>(q.x), q.packed, q.absmax,
-                                         static_cast<const uint16_t *>(q.bias), static_cast<uint16_t *>(q.y), q.ldx,
-                                         q.ldy, static_cast<int>(q.M), static_cast<int>(q.K), static_cast<int>(q.N),
-                                         0, 0};
+                                         static_cast<const uint16_t *>(q.bias), static_cast<uint16_t *>(q.y),
+                                         static_cast<uint16_t *>(q.y2), q.ldx, q.ldy, gc > 0 ? q.ldy2 : 0,
+                                         static_cast<int>(q.M), static_cast<int>(q.K), static_cast<int>(q.N),
+                                         static_cast<int>(q.N - gc), 0, 0};
   }
   if (batch.count == 0) return ok();
   Code16 c;
   for (int i = 0; i < 16; ++i) c.v[i] = code[i];
   launch_gemm_default(batch, c, static_cast<hipStream_t>(stream));
-  return check_launch("nf4_linear_batched");
+  return check_launch(what);
 }
 
 extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx,

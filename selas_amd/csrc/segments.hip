@@ -315,15 +315,6 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// The same function through 0.5 * (1 + tanh(z)) = 1 / (1 + exp(-2z)): one
-// hardware exponential and one reciprocal instead of tanhf (a few ulp of fp32,
-// below the rounding to a 16-bit output).
-__device__ __forceinline__ float gelu_tanh_fast(float x) {
-  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
-  const float kKappa = 0.044715f;
-  const float z = kBeta * (x + kKappa * x * x * x);
-  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * z));
-}
 
 // out[r, 0:Da] = a[r, :] and out[r, Da:Da+Dm] = gelu(m[r, :]); Da may be 0.
 // Eight 16-bit elements per thread when every row is 16-byte aligned.

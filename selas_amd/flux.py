@@ -75,16 +75,29 @@ def sdpa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.T
     return out.transpose(1, 2).reshape(b, l, h * d)
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """[B, H, L, Dh] -> [B, L, H*Dh]: the fused gfx950 kernel (selas_amd.attention), or SDPA for the
-    shapes it does not take (head dim other than 128, L not a multiple of 128)."""
+    shapes it does not take (head dim other than 128, L not a multiple of 128). ``out``: optional
+    destination with equally spaced rows (returned)."""
     from . import _lib
     from .attention import attention as fused_attention
 
     try:
-        return fused_attention(q, k, v)
+        return fused_attention(q, k, v, out)
     except _lib.Unsupported:
-        return sdpa_attention(q, k, v)
+        a = sdpa_attention(q, k, v)
+        if out is None:
+            return a
+        out.copy_(a)
+        return out
+
+
+def _fused_gelu(w, k) -> bool:
+    """The GELU after the MLP input linears goes into the GEMM epilogue when the unit can do that and the
+    segments are this package's kernels (whose GELU the epilogue reproduces bit for bit)."""
+    from .kernels import Kernels
+
+    return isinstance(k, Kernels) and hasattr(w, "linear_gelu_many")
 
 
 def _linear_pair(w, a, b):
@@ -116,8 +129,14 @@ def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k
     img, hi = k.gated_add_mod(img, i_g1, i_proj, i_sh2, i_sc2, dt, guard)
     txt, ht = k.gated_add_mod(txt, t_g1, t_proj, t_sh2, t_sc2, dt, guard)
     del i_proj, t_proj
-    hi, ht = _linear_pair(w, (hi, "img_mlp.0"), (ht, "txt_mlp.0"))
-    oi, ot = _linear_pair(w, (k.gelu(hi), "img_mlp.2"), (k.gelu(ht), "txt_mlp.2"))
+    if _fused_gelu(w, k):
+        # mlp.0 with the GELU in its epilogue: the same bits as k.gelu of its output
+        (_, hi), (_, ht) = w.linear_gelu_many([(hi, "img_mlp.0", cfg.mlp_hidden, None),
+                                               (ht, "txt_mlp.0", cfg.mlp_hidden, None)])
+    else:
+        hi, ht = _linear_pair(w, (hi, "img_mlp.0"), (ht, "txt_mlp.0"))
+        hi, ht = k.gelu(hi), k.gelu(ht)
+    oi, ot = _linear_pair(w, (hi, "img_mlp.2"), (ht, "txt_mlp.2"))
     img = k.gated_add(img, i_g2, oi, guard)
     txt = k.gated_add(txt, t_g2, ot, guard)
     return img, txt
@@ -127,6 +146,20 @@ def single_block(w, x, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kerne
     """x [B, Lt+Li, D] fp32, mod [B, 3D]."""
     sh, sc, g = mod.float().unsqueeze(1).chunk(3, dim=-1)
     f32 = torch.float32
+    if _fused_gelu(w, k):
+        # linear1 writes its MLP columns, GELU'd, straight into linear2's input [attention | GELU(mlp)] and
+        # the attention its output into the first columns: the bits of k.attn_mlp without its round trip.
+        b, l, d = x.shape
+        cat = torch.empty(b, l, d + cfg.mlp_hidden, dtype=dt, device=x.device)
+        ((qkv, _),) = w.linear_gelu_many([(k.mod_in(x, sh, sc, dt), "linear1", cfg.mlp_hidden, cat[..., d:])])
+        q, kk, v = k.qkv_single(qkv, w.get("norm.query_norm.scale", f32), w.get("norm.key_norm.scale", f32), cos,
+                                sin, cfg.heads, dt)
+        del qkv
+        attention(q, kk, v, out=cat[..., :d])
+        del q, kk, v
+        out = w.linear(cat, "linear2")
+        del cat
+        return k.gated_add(x, g, out, guard)
     h = w.linear(k.mod_in(x, sh, sc, dt), "linear1")
     qkv, mlp = h.split([3 * cfg.hidden, cfg.mlp_hidden], dim=-1)
     q, kk, v = k.qkv_single(qkv, w.get("norm.query_norm.scale", f32), w.get("norm.key_norm.scale", f32), cos, sin,

@@ -115,6 +115,83 @@ def _batched_chunk(problems):
     return outs
 
 
+def nf4_linear_gelu(problems) -> list[torch.Tensor | None]:
+    """Tiled NF4 linears whose last output columns go through GELU, up to 4 per launch.
+
+    ``problems``: (x, packed, absmax, blocksize, code, shape, bias, gelu_cols, gelu_out) tuples. For each, the
+    first N - gelu_cols columns of ``x @ W.T + b`` are returned as a new tensor (None when gelu_cols == N), and
+    ``gelu_out`` ([..., gelu_cols], unit column stride, equally spaced rows; allocated when None) receives
+    ``gelu_tanh`` of the other columns, applied to their bf16 values: the bits of ``nf4_linear`` followed by
+    the GELU segment (flux.py:194-200), without the round trip through memory. When the fused epilogue does not
+    take a problem (rows <= 32, N - gelu_cols not a multiple of 256, shapes outside the tiled GEMM), that
+    composition runs instead.
+    """
+    problems = list(problems)
+    outs = []
+    for i in range(0, len(problems), _lib.MAX_BATCHED_LINEARS):
+        outs += _gelu_chunk(problems[i:i + _lib.MAX_BATCHED_LINEARS])
+    return outs
+
+
+def _gelu_composed(x, packed, absmax, blocksize, code, shape, bias, gelu_cols, gelu_out):
+    from .kernels import Kernels
+
+    n = int(shape[0])
+    y = nf4_linear(x, packed, absmax, blocksize, code, shape, bias)
+    g = Kernels().gelu(y[..., n - gelu_cols:])
+    if gelu_out is None:
+        gelu_out = g
+    else:
+        gelu_out.copy_(g)
+    return (y[..., :n - gelu_cols].contiguous() if gelu_cols < n else None), gelu_out
+
+
+def _gelu_chunk(problems):
+    codes = {tuple(float(c) for c in p[4]) for p in problems}
+    if len(codes) != 1 or any(p[0].dtype != torch.bfloat16 or int(p[3]) != 64 for p in problems):
+        return [_gelu_composed(*p) for p in problems]
+    dev = _lib.require_gpu(*(p[0] for p in problems), *(p[1] for p in problems))
+    arr = (_lib.GemmProblem * len(problems))()
+    outs, keep = [], []
+    for i, (x, packed, absmax, _, _, shape, bias, gelu_cols, gelu_out) in enumerate(problems):
+        n, k = int(shape[0]), int(shape[1])
+        gc = int(gelu_cols)
+        if len(shape) != 2 or x.shape[-1] != k or not 0 < gc <= n:
+            raise ValueError(f"x has {x.shape[-1]} features, weight {tuple(shape)} expects {k}; gelu_cols {gc} "
+                             f"must be in (0, {n}]")
+        x2 = _rows(x)
+        if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
+            bias = bias.to(x.dtype).contiguous()
+        y = torch.empty(*x.shape[:-1], n - gc, dtype=x.dtype, device=dev) if gc < n else None
+        if gelu_out is None:
+            gelu_out = torch.empty(*x.shape[:-1], gc, dtype=x.dtype, device=dev)
+        g2 = gelu_out if gelu_out.dim() == 2 else gelu_out.reshape(-1, gc) if gelu_out.is_contiguous() else None
+        if g2 is None:
+            lead = gelu_out.shape[:-1]
+            if gelu_out.stride(-1) != 1 or any(gelu_out.stride(j) != gelu_out.stride(j + 1) * lead[j + 1]
+                                               for j in range(len(lead) - 1)):
+                raise ValueError(f"gelu_out rows must be equally spaced with unit column stride, strides "
+                                 f"{gelu_out.stride()}")
+            ldg = gelu_out.stride(-2)
+        else:
+            ldg = g2.stride(0)
+        if gelu_out.shape[:-1] != x.shape[:-1] or gelu_out.shape[-1] != gc or gelu_out.dtype != x.dtype:
+            raise ValueError(f"gelu_out must be {tuple(x.shape[:-1]) + (gc,)} {x.dtype}, got "
+                             f"{tuple(gelu_out.shape)} {gelu_out.dtype}")
+        keep += [x2, bias]
+        outs.append((y, gelu_out))
+        arr[i] = _lib.GemmProblem(x2.data_ptr(), x2.shape[0], k, x2.stride(0), packed.data_ptr(), absmax.data_ptr(), n,
+                                  _lib.ptr(bias), _lib.ptr(y), n - gc, gelu_out.data_ptr(), ldg, gc)
+    try:
+        with torch.cuda.device(dev):
+            _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), len(problems), 64,
+                      _lib.code_array(next(iter(codes))), _lib.BF16, _lib.stream(dev))
+    except _lib.Unsupported:
+        return [_gelu_composed(*p[:8], o) for p, (_, o) in zip(problems, outs)]
+    del keep
+    return outs
+
+
 class GroupedPlan:
     """A prepared grouped skinny launch: fixed NF4 weights, any x with ``rows`` rows.
 
@@ -243,6 +320,31 @@ class UnitView:
             b = self.get(bname, dtype) if bname in self.tensors else None
             probs.append((x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"], e.shape, b))
         return nf4_linear_batched(probs)
+
+    def linear_gelu_many(self, items, dtype: torch.dtype | None = None) -> list:
+        """For (x, prefix, gelu_cols, gelu_out) items: ``nf4_linear_gelu`` of the unit's weights (the NF4 ones in one
+        launch); returns (plain columns or None, gelu_out) per item."""
+        dtype = dtype or self.dtype
+        fused, results = [], []
+        for x, prefix, gc, out in items:
+            e = self.tensors[prefix + ".weight"]
+            bname = prefix + ".bias"
+            b = self.get(bname, dtype) if bname in self.tensors else None
+            if e.codec == "nf4" and x.dtype == dtype:
+                fused.append((x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"],
+                              e.shape, b, gc, out))
+                results.append(None)
+            else:  # raw weights: the linear, then the GELU segment
+                from .kernels import Kernels
+
+                y = self.linear(x, prefix, dtype)
+                n = y.shape[-1]
+                g = Kernels().gelu(y[..., n - gc:])
+                if out is not None:
+                    out.copy_(g)
+                results.append((y[..., :n - gc].contiguous() if gc < n else None, out if out is not None else g))
+        done = iter(nf4_linear_gelu(fused))
+        return [next(done) if r is None else r for r in results]
 
     def linear(self, x: torch.Tensor, prefix: str, dtype: torch.dtype | None = None) -> torch.Tensor:
         dtype = dtype or self.dtype

@@ -91,3 +91,19 @@ def test_segment_stride_helpers():
     assert kernels.Kernels._rows2(h[..., 9:], "h") == (6, 12, 21)
     with pytest.raises(ValueError):
         kernels._bld(torch.zeros(4, 4).t(), "x")
+
+
+def test_gelu_columns_are_checked():
+    # Validation before any device work: the GELU columns must start at a multiple of the 256-column tile.
+    x = ctypes.c_void_p(4096)
+    arr = (_lib.GemmProblem * 1)()
+    arr[0] = _lib.GemmProblem(4096, 64, 64, 64, 4096, 4096, 512, None, 4096, 512, 4096, 300, 300)
+    with pytest.raises(_lib.Unsupported, match="multiple of 256"):
+        _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), 1, 64, _code(), _lib.BF16, None)
+    arr[0].gelu_cols = 600
+    with pytest.raises(ValueError, match="gelu_cols"):
+        _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), 1, 64, _code(), _lib.BF16, None)
+    arr[0].gelu_cols, arr[0].y2 = 256, None
+    with pytest.raises(ValueError, match="y2"):
+        _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), 1, 64, _code(), _lib.BF16, None)
+    del x

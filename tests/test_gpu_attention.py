@@ -107,3 +107,13 @@ def test_unsupported_shapes_fall_back_to_sdpa(dev):
         y = F.attention(q, k, v)
         assert y.shape == (1, l, 2 * d)
         check_close(y, reference(q, k, v))
+
+
+def test_attention_into_strided_rows(dev):
+    # Output written into the first H*Dh columns of a wider buffer (linear2's input in the single block).
+    q, k, v = qkv(2, 3, 256, 13)
+    wide = torch.zeros(2, 256, 3 * 128 + 200, dtype=torch.bfloat16, device=dev)
+    y = attention(q, k, v, out=wide[..., :3 * 128])
+    assert y.data_ptr() == wide.data_ptr()
+    assert torch.equal(wide[..., :3 * 128], attention(q, k, v))
+    assert torch.count_nonzero(wide[..., 3 * 128:]) == 0

@@ -123,3 +123,24 @@ def test_batched_step_equals_images_one_by_one(model):
         one = model.step(lat[i:i + 1].to(dev), txt[i:i + 1].to(dev), [m[s] for m in mods[i]], fmod[i:i + 1].to(dev),
                          *args)
         assert rel(out[i:i + 1], one.cpu()) < 1e-3
+
+
+def test_fused_gelu_blocks_equal_composed_blocks(model, monkeypatch):
+    # linear1 / mlp.0 with GELU in the GEMM epilogue, written into linear2's input next to the attention
+    # output, against the unfused sequence (linear, GELU kernel, attention, concat): bit for bit.
+    img, txt, cos, sin = inputs(2, 64, 8)
+    dev = torch.device("cuda")
+    img, txt, cos, sin = img.to(dev), txt.to(dev), cos.to(dev), sin.to(dev)
+    dmod = (torch.randn(2, 12 * CFG.hidden, generator=seeded(28)) * 0.3).to(torch.bfloat16).to(dev)
+    smod = (torch.randn(2, 3 * CFG.hidden, generator=seeded(29)) * 0.3).to(torch.bfloat16).to(dev)
+    x = torch.cat((txt, img), dim=1)
+
+    def run():
+        d = F.double_block(model.doubles[1], img, txt, dmod, cos, sin, CFG, torch.bfloat16, False)
+        return d + (F.single_block(model.singles[1], x, smod, cos, sin, CFG, torch.bfloat16, False),)
+
+    fused = run()
+    monkeypatch.setattr(F, "_fused_gelu", lambda w, k: False)
+    composed = run()
+    for a, b in zip(fused, composed):
+        assert torch.equal(a, b)

@@ -204,3 +204,25 @@ def test_batched_equals_one_by_one(dev):
     y0, y1 = nf4_linear_batched(mixed)
     assert torch.equal(y0, nf4_linear(*probs[0])) and torch.equal(y1, nf4_linear(*mixed[1]))
 
+
+
+@pytest.mark.parametrize("m,n,k,gc", [(300, 1280, 640, 512), (100, 256, 128, 256), (513, 2304, 3072, 1792),
+                                      (40, 768, 64, 512), (20, 512, 256, 256), (64, 300, 128, 45)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gelu_epilogue_equals_linear_then_gelu(dev, m, n, k, gc, with_bias):
+    # The last gc output columns GELU'd in the GEMM epilogue, written into a strided destination, against
+    # nf4_linear followed by the GELU segment kernel: the same bits. (20 rows: skinny path; 300 - 45 plain columns,
+    # not a multiple of 256: both take the composed fallback.)
+    from selas_amd.kernels import Kernels
+    from selas_amd.linear import nf4_linear_gelu
+
+    p, a, w_ref = make_weight(n, k, m + n + gc, dev)
+    x = torch.randn(m, k, generator=seeded(41)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(42)) * 0.02).to(torch.bfloat16).to(dev) if with_bias else None
+    wide = torch.zeros(m, gc + 64, dtype=torch.bfloat16, device=dev)
+    ((y, g),) = nf4_linear_gelu([(x, p, a, 64, codecs.NF4_CODE, (n, k), b, gc, wide[:, 32:32 + gc])])
+    full = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    assert torch.equal(g, Kernels().gelu(full[:, n - gc:]))
+    assert (y is None) == (gc == n) and (y is None or torch.equal(y, full[:, :n - gc]))
+    assert torch.count_nonzero(wide[:, :32]) == 0 and torch.count_nonzero(wide[:, 32 + gc:]) == 0
+    check_close(full, oracle_linear(x, w_ref, b))

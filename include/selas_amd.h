@@ -13,10 +13,11 @@
  *     last error on the calling thread is returned by selas_last_error().
  *
  * Data formats follow the reference codec (selas/codecs.py:1-16, 58-63,
- * 99-119): NF4 weights are `packed` uint8 [numel/2] (element 2i in the high
+ * 86-119): NF4 weights are `packed` uint8 [numel/2] (element 2i in the high
  * nibble of byte i), `absmax` fp32 [numel/blocksize] over the flattened
  * tensor, and a 16-entry fp32 codebook passed by value from host memory
- * (the tensor's meta["code"]).
+ * (the tensor's meta["code"]); int8_row weights are `q` int8 in the weight's
+ * shape and `scale` fp32, one per row.
  *
  * Kernels are chosen from shapes, dtypes and pointer alignment only and use
  * no atomics, so equal inputs give equal bits on every call.
@@ -70,6 +71,25 @@ int selas_nf4_dequant(const uint8_t *packed, const float *absmax, int64_t n_byte
  */
 int selas_nf4_encode(const float *w, int64_t n, int64_t blocksize, const float code[16], uint8_t *packed,
                      float *absmax, void *stream);
+
+/*
+ * int8_row decode of a weight of `rows` rows of `cols` elements (q int8
+ * [rows, cols], scale fp32 [rows]):
+ *   out[r, c] = dtype(float(q[r, c]) * float(dtype(scale[r])))
+ * i.e. q.to(dtype) * scale.to(dtype) computed in dtype; for bf16 and fp16 the
+ * product is exact in fp32 and rounded once. Bit-identical to the reference
+ * decode (selas/codecs.py:273-277) except NaN payloads.
+ */
+int selas_int8_row_dequant(const int8_t *q, const float *scale, int64_t rows, int64_t cols, void *out,
+                           int out_dtype, void *stream);
+
+/*
+ * int8_row encode of an fp32 weight [rows, cols]: scale[r] = max |w[r, :]| / 127
+ * (1 where that max is not positive), q[r, c] = clamp(round_half_even(w[r, c] /
+ * scale[r]), -127, 127), with IEEE fp32 division.
+ * Replaces encode_int8_row (selas/codecs.py:86-96).
+ */
+int selas_int8_row_encode(const float *w, int64_t rows, int64_t cols, int8_t *q, float *scale, void *stream);
 
 /* ------------------------------------------------------------ linear */
 
@@ -134,6 +154,30 @@ typedef struct selas_nf4_gemm_problem {
  */
 int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
                              const float code[16], int dtype, void *stream);
+
+/*
+ * Quantized linear forward y = x W^T + bias with W an int8_row [N, K] weight
+ * (q int8 [N, K] row-major, 16-byte aligned; scale fp32 [N]); x, bias, y and
+ * dtype as for selas_nf4_linear.
+ * M > 32 runs the tiled MFMA GEMM of selas_nf4_linear with the int8 operand
+ * bf16(q * bf16(scale)), the reference's decoded weight bit for bit. M <= 32
+ * runs a skinny kernel that multiplies x by q exactly and scales the fp32 row
+ * sums by bf16(scale): it agrees with the decoded-weight product to the bf16
+ * rounding of the decoded weight. Returns SELAS_EUNSUPPORTED for K % 64 != 0,
+ * misaligned rows or a dtype other than bf16 (the caller then decodes with
+ * selas_int8_row_dequant and uses a library GEMM).
+ * Replaces UnitView.linear for int8_row weights (selas/store.py:289-293):
+ * decode (codecs.py:273-277) followed by F.linear.
+ */
+int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const int8_t *q, const float *scale,
+                          int64_t N, const void *bias, void *y, int64_t ldy, int dtype, void *stream);
+
+/*
+ * selas_nf4_linear_batched for int8_row weights: in each problem `packed`
+ * holds q and `absmax` the row scales; gelu_cols and y2 as there.
+ * No counterpart in the reference (see selas_nf4_linear_batched).
+ */
+int selas_int8_row_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int dtype, void *stream);
 
 /*
  * One NF4 weight of a grouped skinny linear (device-memory array element).

@@ -23,6 +23,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from . import int8_row as oi8
 from . import nf4 as onf4
 from .segments import OracleKernels, timestep_embedding
 
@@ -61,8 +62,8 @@ class OracleUnit:
     def from_encoded(cls, enc: dict, dtype: torch.dtype, operand_dtype: torch.dtype = torch.bfloat16):
         """From {name: (codec, shape, meta, parts)} with CPU numpy/torch parts.
 
-        NF4 weights decode to ``operand_dtype`` (the compute dtype the reference
-        decodes into) and are held as fp32 values of those bits.
+        NF4 and int8_row weights decode to ``operand_dtype`` (the compute dtype the
+        reference decodes into) and are held as fp32 values of those bits.
         """
         out = {}
         for name, (codec, shape, meta, parts) in enc.items():
@@ -70,6 +71,14 @@ class OracleUnit:
                 vals = onf4.decode(np.asarray(parts["packed"]), np.asarray(parts["absmax"]), int(meta["blocksize"]),
                                    meta["code"], onf4.F32)
                 w = torch.from_numpy(vals).view(*shape).to(operand_dtype).float()
+            elif codec == "int8_row":
+                out_code = {torch.bfloat16: oi8.BF16, torch.float16: oi8.F16, torch.float32: oi8.F32}[operand_dtype]
+                vals = oi8.decode(np.asarray(parts["q"]), np.asarray(parts["scale"]), out_code)
+                if out_code == oi8.BF16:
+                    vals = onf4.bf16_to_f32(vals)
+                elif out_code == oi8.F16:
+                    vals = vals.view(np.float16).astype(np.float32)
+                w = torch.from_numpy(np.ascontiguousarray(vals)).view(*shape).float()
             else:
                 w = torch.as_tensor(parts["data"]).float()
             out[name] = w

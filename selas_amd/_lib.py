@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libselas_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
@@ -30,6 +30,10 @@ SIGNATURES: dict[str, list] = {
     "selas_nf4_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _F16x, _I64, _P, _P, _I64, _INT, _P],
     "selas_nf4_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F16x, _INT, _P],
     "selas_nf4_linear_batched": [_P, _I64, _I64, _F16x, _INT, _P],
+    "selas_int8_row_dequant": [_P, _P, _I64, _I64, _P, _INT, _P],
+    "selas_int8_row_encode": [_P, _I64, _I64, _P, _P, _P],
+    "selas_int8_row_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _INT, _P],
+    "selas_int8_row_linear_batched": [_P, _I64, _INT, _P],
     "selas_mod_in": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _INT, _P],
     "selas_gated_add": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P],
     "selas_gated_add_mod": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P, _I64,

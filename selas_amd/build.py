@@ -18,7 +18,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libselas_amd.so"
-SOURCES = ("errors.hip", "nf4_codec.hip", "nf4_linear.hip", "segments.hip", "attention.hip")
+SOURCES = ("errors.hip", "nf4_codec.hip", "int8_row_codec.hip", "nf4_linear.hip", "segments.hip", "attention.hip")
 ARCH = "gfx950"
 
 # Packed-fp32 instructions are switched off for all device code: hipcc still

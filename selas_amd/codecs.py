@@ -133,15 +133,59 @@ def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, blocksize: int, code
     return out.view(tuple(shape))
 
 
+def encode_int8_row(name: str, t: torch.Tensor) -> EncodedTensor:
+    """int8_row-encodes ``t`` (selas/codecs.py:86-96) with the GPU encoder: one fp32 scale per row
+    (absmax / 127, 1 for a zero row) and q = clamp(round(w / scale), -127, 127) in ``t``'s shape.
+
+    Parts live on ``t``'s device; a CPU tensor is encoded on the current GPU and its parts are
+    copied back, as for ``encode_nf4``.
+    """
+    if t.dim() < 2:
+        raise ValueError(f"int8_row needs a matrix, got {tuple(t.shape)} for {name}")
+    dev = _gpu_for(t)
+    rows = int(t.shape[0])
+    cols = t.numel() // rows if rows else 0
+    w = t.detach().to(device=dev, dtype=torch.float32).reshape(rows, cols).contiguous()
+    q = torch.empty(tuple(t.shape), dtype=torch.int8, device=dev)
+    scale = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("selas_int8_row_encode", w.data_ptr(), rows, cols, q.data_ptr(), scale.data_ptr(), _lib.stream(dev))
+    if t.device.type != "cuda":
+        q, scale = q.cpu(), scale.cpu()
+    return EncodedTensor(name, "int8_row", tuple(t.shape), {}, {"q": q, "scale": scale})
+
+
+def int8_row_dequant(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Decodes to ``dtype`` in q's shape: ``q.to(dtype) * scale.to(dtype)`` per row, evaluated in ``dtype``.
+
+    Bit-identical to the reference decode (selas/codecs.py:273-277).
+    """
+    dev = _lib.require_gpu(q, scale)
+    if q.dtype != torch.int8:
+        raise ValueError(f"int8_row data must be int8, got {q.dtype}")
+    if scale.dtype != torch.float32:
+        raise ValueError(f"int8_row scale must be float32, got {scale.dtype}")
+    if q.dim() < 1 or scale.numel() != q.shape[0] or not q.is_contiguous() or not scale.is_contiguous():
+        raise ValueError(f"int8_row parts do not match: q {tuple(q.shape)}, scale {tuple(scale.shape)} "
+                         "(one scale per row, contiguous)")
+    rows = int(q.shape[0])
+    cols = q.numel() // rows if rows else 0
+    out = torch.empty(tuple(q.shape), dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("selas_int8_row_dequant", q.data_ptr(), scale.data_ptr(), rows, cols, out.data_ptr(),
+                  _lib.dtype_code(dtype), _lib.stream(dev))
+    return out
+
+
 def decode(codec: str, parts: dict[str, torch.Tensor], meta: dict, shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
-    """Codec dispatch as selas/codecs.py:269-280 (raw and nf4)."""
+    """Codec dispatch as selas/codecs.py:269-280 (raw, int8_row and nf4)."""
     if codec == "raw":
         x = parts["data"]
         return x if x.dtype == dtype else x.to(dtype)
     if codec == "nf4":
         return nf4_dequant(parts["packed"], parts["absmax"], int(meta["blocksize"]), meta["code"], tuple(shape), dtype)
     if codec == "int8_row":
-        raise NotImplementedError("int8_row decoding is not part of selas_amd's NF4 path")
+        return int8_row_dequant(parts["q"], parts["scale"], dtype)
     raise ValueError(f"unknown codec {codec!r}")
 
 

@@ -171,6 +171,105 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
   }
 }
 
+// ------------------------------------------------------------- int8_row skinny GEMM
+//
+// For M <= 32 with int8_row weights (q [N, K] int8, one fp32 scale per row):
+// y[m, n] = bf16(s_n * sum_k x[m, k] q[n, k] + b_n), s_n = bf16(scale_n). The
+// row scale is applied to the fp32 sums instead of to every weight: the sums
+// are those of the exact quantized weight q * s_n, where the reference's
+// operand bf16(q * s_n) carries one bf16 rounding per element (relative
+// 2^-9 at most). The MFMA operand is the biased byte u = q + 128, exact in
+// bf16 (integers up to 256 are), and sum_k x u - 128 sum_k x = sum_k x q, the
+// second sum coming from one more MFMA against ones.
+//
+// Workgroup: 64 output columns (two 32-column groups), all M rows; the four
+// waves take the K blocks round-robin and their partial results are summed in
+// LDS in wave order (deterministic).
+constexpr int kI8GemvThreads = 256;
+
+__device__ __forceinline__ bf16x8 biased_i8_to_bf16(uint32_t d0, uint32_t d1) {
+  const uint32_t u0 = d0 ^ 0x80808080u, u1 = d1 ^ 0x80808080u;
+  auto f = [](uint32_t u, int j) { return static_cast<float>((u >> (8 * j)) & 0xffu); };
+  uint4 r;
+  r.x = pack_bf16x2(f(u0, 0), f(u0, 1));
+  r.y = pack_bf16x2(f(u0, 2), f(u0, 3));
+  r.z = pack_bf16x2(f(u1, 0), f(u1, 1));
+  r.w = pack_bf16x2(f(u1, 2), f(u1, 3));
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+__global__ __launch_bounds__(kI8GemvThreads) void int8_row_gemv_kernel(
+    const uint16_t *__restrict__ x, int64_t ldx, int M, int K, const int8_t *__restrict__ q,
+    const float *__restrict__ scale, int N, const uint16_t *__restrict__ bias, uint16_t *__restrict__ y,
+    int64_t ldy) {
+  constexpr int G = 2;  // column groups
+  __shared__ float red[4][G * 16][64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c = lane & 31;
+  const int kblocks = K >> 6;
+  const int n_base = blockIdx.x * (32 * G);
+  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 32 * h;
+  const int8_t *wr[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) wr[g] = q + static_cast<int64_t>(min(n_base + 32 * g + c, N - 1)) * K + 32 * h;
+  const uint32_t one2 = 0x3F803F80u;  // two bf16 ones
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(one2, one2, one2, one2));
+
+  f32x16 acc[G], accx = f32x16{};
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = f32x16{};
+  // Two K blocks per iteration (this wave's kb and kb + 4), all loads issued before the MFMAs.
+  auto load = [&](int kb, uint4 (&wq)[G][2], bf16x8 (&xf)[4]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      wq[g][0] = *reinterpret_cast<const uint4 *>(wr[g] + kb * 64);
+      wq[g][1] = *reinterpret_cast<const uint4 *>(wr[g] + kb * 64 + 16);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xf[s] = *reinterpret_cast<const bf16x8 *>(xr + kb * 64 + 8 * s);
+  };
+  auto mul = [&](const uint4 (&wq)[G][2], const bf16x8 (&xf)[4]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      accx = mfma32(xf[s], ones, accx);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint4 &w = wq[g][s >> 1];
+        acc[g] = mfma32(xf[s], biased_i8_to_bf16((s & 1) ? w.z : w.x, (s & 1) ? w.w : w.y), acc[g]);
+      }
+    }
+  };
+  for (int kb = wave; kb < kblocks; kb += 8) {
+    uint4 wa[G][2], wb[G][2];
+    bf16x8 xa[4], xb[4];
+    const bool two = kb + 4 < kblocks;
+    load(kb, wa, xa);
+    load(two ? kb + 4 : kb, wb, xb);
+    mul(wa, xa);
+    if (two) mul(wb, xb);
+  }
+  // Per wave: its partial sum_k x q, in the MFMA layout (row m of lane l, register r:
+  // 8*(r/4) + 4*(l/32) + r%4; column l%32).
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][g * 16 + r][lane] = acc[g][r] - 128.0f * accx[r];
+  __syncthreads();
+  for (int e = tid; e < G * 16 * 64; e += kI8GemvThreads) {
+    const int l = e & 63, gr = e >> 6;
+    const float v = ((red[0][gr][l] + red[1][gr][l]) + red[2][gr][l]) + red[3][gr][l];
+    const int g = gr >> 4, r = gr & 15;
+    const int m = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const int n = n_base + 32 * g + (l & 31);
+    if (m < M && n < N) {
+      const float sb = bf16_bits_to_f32(bf16_bits_rne(scale[n]));
+      const float b = bias ? bf16_bits_to_f32(bias[n]) : 0.0f;
+      y[static_cast<int64_t>(m) * ldy + n] = bf16_bits_rne(sb * v + b);
+    }
+  }
+}
+
 // ------------------------------------------------------------- streaming skinny GEMM
 //
 // For M <= 32 and K = 1024, 2048, 3072 (the hoisted modulation linears have
@@ -694,6 +793,40 @@ __device__ __forceinline__ void interleave_substep() {
 //   * before sub-step 3 the block kb+1 loads are waited for and the
 //     workgroup synchronises; sub-step 3 then overlaps with building the
 //     product tables and first fragments of block kb+1.
+// Weight codecs of the tiled GEMM. kNF4: `packed` holds two 4-bit codes per
+// byte, `absmax` one fp32 scale per 64-block. kInt8Row: `packed` holds int8
+// values q [N, K], `absmax` one fp32 scale s per row; the operand is
+// bf16(q * bf16(s)) (selas/codecs.py:273-277 decodes with q.to(bf16) *
+// s.to(bf16)).
+enum class WCodec { kNF4, kInt8Row };
+
+// The per-block weight registers of one wave: CB column groups, one 64-wide K
+// block. NF4: 16 code bytes and the block scale per lane; int8: 32 bytes.
+template <WCodec WC, int CB>
+struct WRegs {
+  uint4 q[CB];
+  float s[CB];
+};
+template <int CB>
+struct WRegs<WCodec::kInt8Row, CB> {
+  uint4 q[CB][2];
+};
+
+// Eight int8 values (dwords d0, d1, element j in byte j % 4 of d(j / 4)) ->
+// bf16(q * sb) in k order, sb = bf16(scale) as fp32 and nb = -128 * sb. The
+// biased byte u = q + 128 converts exactly to fp32 and fma(u, sb, nb) is the
+// exact product q * sb (at most 16 significant bits), rounded once to bf16.
+__device__ __forceinline__ bf16x8 dequant8_i8(uint32_t d0, uint32_t d1, float sb, float nb) {
+  const uint32_t u0 = d0 ^ 0x80808080u, u1 = d1 ^ 0x80808080u;
+  auto f = [&](uint32_t u, int j) { return __builtin_fmaf(static_cast<float>((u >> (8 * j)) & 0xffu), sb, nb); };
+  uint4 r;
+  r.x = pack_bf16x2(f(u0, 0), f(u0, 1));
+  r.y = pack_bf16x2(f(u0, 2), f(u0, 3));
+  r.z = pack_bf16x2(f(u1, 0), f(u1, 1));
+  r.w = pack_bf16x2(f(u1, 2), f(u1, 3));
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 // One problem of a batched launch; its tiles are global tiles [tile0, tile0 + tiles_m * tiles_n).
 // Output columns [n_split, N) are written as bf16(gelu_tanh(bf16(acc + bias)))
 // to Y2 at column n - n_split (row stride ldy2); n_split is N (no such columns)
@@ -713,8 +846,10 @@ struct GemmBatch {
   int count, tiles, per_xcd;
 };
 
-template <int MB, int CB, int STAGES, int NW>
-__global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
+template <WCodec WC, int MB, int CB, int STAGES, int NW>
+__device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) {
+  constexpr bool kI8 = WC == WCodec::kInt8Row;
+  using WR = WRegs<WC, CB>;
   constexpr int TM = 32 * MB, WN = 32 * CB, TN = NW * WN;
   constexpr int SB = TM * 128;      // bytes of one x stage: TM rows x 64 bf16
   constexpr int LOOK = STAGES - 1;
@@ -748,8 +883,10 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
   // Buffer resources; the range check covers the per-lane offset, which holds
   // the row term, so rows past M or N read as zeros (never stored).
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(X, static_cast<uint32_t>(M) * ldx_b);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(packed, static_cast<uint32_t>(N) * static_cast<uint32_t>(K >> 1));
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(absmax, static_cast<uint32_t>(N) * static_cast<uint32_t>(kblocks) * 4u);
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(packed, static_cast<uint32_t>(N) * static_cast<uint32_t>(kI8 ? K : (K >> 1)));
+  const __amdgpu_buffer_rsrc_t sr =
+      make_rsrc(absmax, static_cast<uint32_t>(N) * static_cast<uint32_t>(kI8 ? 1 : kblocks) * 4u);
 
   // x tile DMA: wave w fills tile rows [8*XL*w, 8*XL*(w+1)) with XL loads of 8
   // rows; lane i of load j lands at row r = 8*XL*w + 8j + i/8, physical
@@ -770,8 +907,22 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     const uint32_t n = static_cast<uint32_t>(n0 + WN * wave + 32 * cb + c);
-    b_voff[cb] = n * static_cast<uint32_t>(K >> 1) + 16u * h;
-    s_voff[cb] = n * static_cast<uint32_t>(kblocks) * 4u;
+    if constexpr (kI8) {
+      b_voff[cb] = n * static_cast<uint32_t>(K) + 32u * h;
+      s_voff[cb] = n * 4u;
+    } else {
+      b_voff[cb] = n * static_cast<uint32_t>(K >> 1) + 16u * h;
+      s_voff[cb] = n * static_cast<uint32_t>(kblocks) * 4u;
+    }
+  }
+  // int8: the row scale, bf16-rounded as the reference's decode rounds it, and -128 times it.
+  float sb[CB], nb[CB];
+  if constexpr (kI8) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      sb[cb] = bf16_bits_to_f32(bf16_bits_rne(load_f32(sr, s_voff[cb], 0)));
+      nb[cb] = -128.0f * sb[cb];
+    }
   }
   float cl[8];
 #pragma unroll
@@ -783,13 +934,21 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
 
   // Loads block `blk` into LDS stage `stage` and the registers bq/bs; the
   // register loads go first so that later uses of them do not wait for the DMA.
-  auto issue = [&](int stage, int blk, uint4 (&bq)[CB], float (&bs)[CB]) {
-    const uint32_t kb = static_cast<uint32_t>(blk);
+  auto load_w = [&](uint32_t kb, WR &w) {
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      bq[cb] = load_b128(wr, b_voff[cb], kb * 32u);
-      bs[cb] = load_f32(sr, s_voff[cb], kb * 4u);
+      if constexpr (kI8) {
+        w.q[cb][0] = load_b128(wr, b_voff[cb], kb * 64u);
+        w.q[cb][1] = load_b128(wr, b_voff[cb], kb * 64u + 16u);
+      } else {
+        w.q[cb] = load_b128(wr, b_voff[cb], kb * 32u);
+        w.s[cb] = load_f32(sr, s_voff[cb], kb * 4u);
+      }
     }
+  };
+  auto issue = [&](int stage, int blk, WR &w) {
+    const uint32_t kb = static_cast<uint32_t>(blk);
+    load_w(kb, w);
     uint8_t *dst = a_dst + stage * SB;
 #pragma unroll
     for (int j = 0; j < XL; ++j) load_lds16(xr, dst + j * 1024, a_voff[j & 1] + j * a_vstep, kb * 128u);
@@ -799,15 +958,9 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
   // unit instead of overlapping the MFMAs): part 0 the codes, scales and the
   // first x loads, parts 1-3 the rest of the x tile (x load j in part 4j/XL).
   constexpr int P3 = XL - (3 * XL + 3) / 4;  // x loads in part 3
-  auto issue_part = [&](int stage, int blk, int part, uint4 (&bq)[CB], float (&bs)[CB]) {
+  auto issue_part = [&](int stage, int blk, int part, WR &w) {
     const uint32_t kb = static_cast<uint32_t>(blk);
-    if (part == 0) {
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        bq[cb] = load_b128(wr, b_voff[cb], kb * 32u);
-        bs[cb] = load_f32(sr, s_voff[cb], kb * 4u);
-      }
-    }
+    if (part == 0) load_w(kb, w);
     uint8_t *dst = a_dst + stage * SB;
 #pragma unroll
     for (int j = (part * XL + 3) / 4; j < ((part + 1) * XL + 3) / 4; ++j)
@@ -817,6 +970,15 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
     return *reinterpret_cast<const bf16x8 *>(smem + (kb % STAGES) * SB + a_rd[s] + mb * 4096);
   };
   auto word = [](const uint4 &q, int s) { return s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w; };
+  // Weight fragment of column group cb for sub-step s (k in [32h + 8s, 32h + 8s + 8) of the block).
+  auto wfrag = [&](const WR &w, int cb, int s, const Tables &t) -> bf16x8 {
+    if constexpr (kI8) {
+      const uint4 &q = w.q[cb][s >> 1];
+      return dequant8_i8((s & 1) ? q.z : q.x, (s & 1) ? q.w : q.y, sb[cb], nb[cb]);
+    } else {
+      return dequant8(t, word(w.q[cb], s));
+    }
+  };
 
   f32x16 acc[MB][CB];
 #pragma unroll
@@ -827,11 +989,10 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
   // Every iteration issues the loads of block kb+LOOK; past the last block the
   // last block is loaded again (valid addresses, into the stage that is free)
   // so that the loop body has no branches and schedules as one region.
-  uint4 bq0[CB], bq1[CB], bq2[CB];
-  float bs0[CB], bs1[CB], bs2[CB];
-  issue(0, 0, bq0, bs0);
+  WR w0, w1, w2;
+  issue(0, 0, w0);
   if constexpr (STAGES == 3) {
-    issue(1, min(1, kblocks - 1), bq1, bs1);
+    issue(1, min(1, kblocks - 1), w1);
     wait_vmcnt<LPB>();
   } else {
     wait_vmcnt<0>();
@@ -842,45 +1003,44 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
   Tables tab[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    tab[cb] = make_tables(cl, bs0[cb]);
-    wf[0][cb] = dequant8(tab[cb], word(bq0[cb], 0));
+    if constexpr (!kI8) tab[cb] = make_tables(cl, w0.s[cb]);
+    wf[0][cb] = wfrag(w0, cb, 0, tab[cb]);
   }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) af[mb] = frag(0, 0, mb);
 
-  // One K block. cq holds block kb's codes, nq/ns block kb+1's, fq/fs receive
-  // block kb+LOOK's (with one block of lookahead that is nq/ns itself). The
-  // loop below is unrolled STAGES times so that the register sets rotate by
-  // name, never by copying registers that a load in flight still targets.
-  auto block = [&](int kb, const uint4 (&cq)[CB], const uint4 (&nq)[CB], const float (&ns)[CB], uint4 (&fq)[CB],
-                   float (&fs)[CB]) {
+  // One K block. cw holds block kb's weights, nw block kb+1's, fw receives
+  // block kb+LOOK's (with one block of lookahead that is nw itself). The loop
+  // below is unrolled STAGES times so that the register sets rotate by name,
+  // never by copying registers that a load in flight still targets.
+  auto block = [&](int kb, const WR &cw, const WR &nw, WR &fw) {
     const int fstage = (kb + LOOK) % STAGES, fblk = min(kb + LOOK, kblocks - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
       if (s < 3) {
         if constexpr (LOOK >= 2) {
-          issue_part(fstage, fblk, s, fq, fs);
+          issue_part(fstage, fblk, s, fw);
         } else if (s == 0) {
 #pragma unroll
-          for (int part = 0; part < 4; ++part) issue_part(fstage, fblk, part, fq, fs);
+          for (int part = 0; part < 4; ++part) issue_part(fstage, fblk, part, fw);
         }
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) wf[nxt][cb] = dequant8(tab[cb], word(cq[cb], s + 1));
+        for (int cb = 0; cb < CB; ++cb) wf[nxt][cb] = wfrag(cw, cb, s + 1, tab[cb]);
       } else {
         if constexpr (LOOK >= 2) {
           // Block kb+1's loads are older than parts 0-2 of block kb+LOOK's.
           wait_vmcnt<(LOOK - 1) * LPB - P3>();
           lds_barrier();
-          issue_part(fstage, fblk, 3, fq, fs);
+          issue_part(fstage, fblk, 3, fw);
         } else {
           wait_vmcnt<0>();
           lds_barrier();
         }
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
-          tab[cb] = make_tables(cl, ns[cb]);
-          wf[nxt][cb] = dequant8(tab[cb], word(nq[cb], 0));
+          if constexpr (!kI8) tab[cb] = make_tables(cl, nw.s[cb]);
+          wf[nxt][cb] = wfrag(nw, cb, 0, tab[cb]);
         }
       }
 #pragma unroll
@@ -890,29 +1050,30 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
         af[mb] = s < 3 ? frag(kb, s + 1, mb) : frag(kb + 1, 0, mb);
       }
       constexpr int F = MB * CB;  // MFMAs per sub-step
-      if (s < 3) interleave_substep<F, CB, (26 * CB + F - 1) / F + 1>();
-      else interleave_substep<F, CB, (50 * CB + F - 1) / F + 1>();
+      // VALU per column group and sub-step: NF4 26 (50 with the product tables), int8 22.
+      constexpr int VS = kI8 ? 22 : 26, VL = kI8 ? 22 : 50;
+      if (s < 3) interleave_substep<F, CB, (VS * CB + F - 1) / F + 1>();
+      else interleave_substep<F, CB, (VL * CB + F - 1) / F + 1>();
     }
   };
 
   int kb = 0;
   if constexpr (STAGES == 3) {
     for (; kb + 3 <= kblocks; kb += 3) {
-      block(kb, bq0, bq1, bs1, bq2, bs2);
-      block(kb + 1, bq1, bq2, bs2, bq0, bs0);
-      block(kb + 2, bq2, bq0, bs0, bq1, bs1);
+      block(kb, w0, w1, w2);
+      block(kb + 1, w1, w2, w0);
+      block(kb + 2, w2, w0, w1);
     }
-    if (kb < kblocks) block(kb, bq0, bq1, bs1, bq2, bs2);
-    if (kb + 1 < kblocks) block(kb + 1, bq1, bq2, bs2, bq0, bs0);
+    if (kb < kblocks) block(kb, w0, w1, w2);
+    if (kb + 1 < kblocks) block(kb + 1, w1, w2, w0);
   } else {
     for (; kb + 2 <= kblocks; kb += 2) {
-      block(kb, bq0, bq1, bs1, bq1, bs1);
-      block(kb + 1, bq1, bq0, bs0, bq0, bs0);
+      block(kb, w0, w1, w1);
+      block(kb + 1, w1, w0, w0);
     }
-    if (kb < kblocks) block(kb, bq0, bq1, bs1, bq1, bs1);
+    if (kb < kblocks) block(kb, w0, w1, w1);
   }
-  (void)bq2;
-  (void)bs2;
+  (void)w2;
 
   // Epilogue: acc[mb][cb] holds D[n][m] for n = n0 + WN*wave + 32*cb + 8*(r/4) + 4*h + r%4
   // and m = m0 + 32*mb + c. Bias is added in fp32 and the sum rounded once.
@@ -1017,9 +1178,18 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, C
   }
 }
 
+template <int MB, int CB, int STAGES, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
+  qgemm_body<WCodec::kNF4, MB, CB, STAGES, NW>(batch, code);
+}
+template <int MB, int CB, int STAGES, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void int8_row_gemm_kernel(GemmBatch batch) {
+  qgemm_body<WCodec::kInt8Row, MB, CB, STAGES, NW>(batch, Code16{});
+}
+
 // `batch.p[0..count)` filled except tiles_n / tile0, which are set here.
 template <int MB, int CB, int STAGES, int NW>
-void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s) {
+void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4) {
   int64_t tiles = 0;
   for (int i = 0; i < batch.count; ++i) {
     GemmProblem &p = batch.p[i];
@@ -1030,13 +1200,17 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s) {
   }
   batch.tiles = static_cast<int>(tiles);
   batch.per_xcd = static_cast<int>(cdiv(tiles, 8));
-  nf4_gemm_kernel<MB, CB, STAGES, NW><<<dim3(static_cast<uint32_t>(batch.per_xcd * 8)), dim3(64 * NW), 0, s>>>(batch, c);
+  const dim3 grid(static_cast<uint32_t>(batch.per_xcd * 8)), block(64 * NW);
+  if (wc == WCodec::kInt8Row) int8_row_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch);
+  else nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
 }
 
 // Every launch uses 256 x 256 tiles of 4 waves (256 x 64 each), 3 LDS stages.
 // 128 x 512 tiles of 8 waves (128 x 64 each, two waves per SIMD) measured 15-25 %
 // slower: each decoded weight fragment then serves 4 MFMAs instead of 8.
-void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s) { launch_gemm<8, 2, 3, 4>(batch, c, s); }
+void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4) {
+  launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
+}
 
 }  // namespace
 }  // namespace selas
@@ -1046,9 +1220,12 @@ using namespace selas;
 namespace {
 // Validation shared by the single and batched entries: SELAS_OK when the fused
 // kernels take the call, or the error (EUNSUPPORTED: the caller falls back).
+// For int8_row weights `packed` is q [N, K] and `absmax` the N row scales;
+// blocksize and code are not used.
 int check_linear(const char *what, const void *x, int64_t M, int64_t K, int64_t ldx, const uint8_t *packed,
                  const float *absmax, int64_t blocksize, const float *code, int64_t N, const void *bias,
-                 const void *y, int64_t ldy, int dtype) {
+                 const void *y, int64_t ldy, int dtype, WCodec wc = WCodec::kNF4) {
+  const bool i8 = wc == WCodec::kInt8Row;
   if (M < 0 || K <= 0 || N <= 0)
     return set_error(SELAS_EINVAL, "%s: bad shape M=%lld K=%lld N=%lld", what, (long long)M, (long long)K,
                      (long long)N);
@@ -1057,10 +1234,12 @@ int check_linear(const char *what, const void *x, int64_t M, int64_t K, int64_t 
     return set_error(SELAS_EINVAL, "%s: row strides ldx=%lld ldy=%lld below K, N", what, (long long)ldx,
                      (long long)ldy);
   if (M == 0) return SELAS_OK;
-  if (!x || !packed || !absmax || !y || !code) return set_error(SELAS_EINVAL, "%s: null pointer", what);
+  if (!x || !packed || !absmax || !y || (!code && !i8)) return set_error(SELAS_EINVAL, "%s: null pointer", what);
   if (dtype != SELAS_BF16)
     return set_error(SELAS_EUNSUPPORTED, "%s: fused kernels take bf16, got %s", what, dtype_name(dtype));
-  if (blocksize != 64 || K % 64)
+  if (i8 && K % 64)
+    return set_error(SELAS_EUNSUPPORTED, "%s: fused kernels need K %% 64 == 0 (K %lld)", what, (long long)K);
+  if (!i8 && (blocksize != 64 || K % 64))
     return set_error(SELAS_EUNSUPPORTED, "%s: fused kernels need blocksize 64 and K %% 64 == 0 (blocksize %lld, K %lld)",
                      what, (long long)blocksize, (long long)K);
   if (!aligned(x, 16) || ldx % 8 || !aligned(packed, 16) || !aligned(absmax, 4) || !aligned(y, 8) || ldy % 4 ||
@@ -1069,7 +1248,8 @@ int check_linear(const char *what, const void *x, int64_t M, int64_t K, int64_t 
                                          "8-byte aligned y rows", what);
   // Buffer offsets are 32-bit: every operand (plus one tile of overhang) must span < 4 GiB.
   const int64_t lim = (1ll << 32) - 1;
-  if ((M + 512) * ldx * 2 > lim || (N + 256) * (K / 2) > lim || (N + 256) * (K / 64) * 4 > lim || M * ldy * 2 > lim)
+  if ((M + 512) * ldx * 2 > lim || (N + 256) * (i8 ? K : K / 2) > lim || (N + 256) * (i8 ? 1 : K / 64) * 4 > lim ||
+      M * ldy * 2 > lim)
     return set_error(SELAS_EUNSUPPORTED, "%s: operand above 4 GiB", what);
   return SELAS_OK;
 }
@@ -1106,10 +1286,10 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
   return check_launch("nf4_linear (gemm)");
 }
 
-extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
-                                        const float code[16], int dtype, void *stream) {
+namespace {
+int linear_batched(const char *what, WCodec wc, const selas_nf4_gemm_problem *problems, int64_t count,
+                   int64_t blocksize, const float *code, int dtype, void *stream) {
   static_assert(kGemmMaxProblems == SELAS_MAX_BATCHED_LINEARS, "batch size");
-  const char *what = "nf4_linear_batched";
   if (count < 0 || count > kGemmMaxProblems)
     return set_error(SELAS_EINVAL, "%s: count %lld outside [0, %d]", what, (long long)count, kGemmMaxProblems);
   if (count > 0 && !problems) return set_error(SELAS_EINVAL, "%s: null problems", what);
@@ -1124,7 +1304,7 @@ extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, 
     const void *y = (gc == q.N && gc > 0 && !q.y) ? q.y2 : q.y;
     const int64_t ldy_chk = gc > 0 ? std::max<int64_t>(q.ldy, q.N) : q.ldy;
     if (int e = check_linear(what, q.x, q.M, q.K, q.ldx, q.packed, q.absmax, blocksize, code, q.N, q.bias, y, ldy_chk,
-                             dtype))
+                             dtype, wc))
       return e;
     if (gc > 0 && gc < q.N && q.ldy < q.N - gc)
       return set_error(SELAS_EINVAL, "%s: ldy %lld below the %lld plain columns", what, (long long)q.ldy,
@@ -1146,10 +1326,48 @@ extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, 
                                          static_cast<int>(q.N - gc), 0, 0};
   }
   if (batch.count == 0) return ok();
-  Code16 c;
-  for (int i = 0; i < 16; ++i) c.v[i] = code[i];
-  launch_gemm_default(batch, c, static_cast<hipStream_t>(stream));
+  Code16 c{};
+  if (wc == WCodec::kNF4)
+    for (int i = 0; i < 16; ++i) c.v[i] = code[i];
+  launch_gemm_default(batch, c, static_cast<hipStream_t>(stream), wc);
   return check_launch(what);
+}
+}  // namespace
+
+extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
+                                        const float code[16], int dtype, void *stream) {
+  return linear_batched("nf4_linear_batched", WCodec::kNF4, problems, count, blocksize, code, dtype, stream);
+}
+
+extern "C" int selas_int8_row_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int dtype,
+                                             void *stream) {
+  return linear_batched("int8_row_linear_batched", WCodec::kInt8Row, problems, count, 0, nullptr, dtype, stream);
+}
+
+extern "C" int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const int8_t *q,
+                                     const float *scale, int64_t N, const void *bias, void *y, int64_t ldy, int dtype,
+                                     void *stream) {
+  const uint8_t *qb = reinterpret_cast<const uint8_t *>(q);
+  if (int e = check_linear("int8_row_linear", x, M, K, ldx, qb, scale, 0, nullptr, N, bias, y, ldy, dtype,
+                           WCodec::kInt8Row))
+    return e;
+  if (M == 0) return ok();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t *xb = static_cast<const uint16_t *>(x);
+  const uint16_t *bb = static_cast<const uint16_t *>(bias);
+  uint16_t *yb = static_cast<uint16_t *>(y);
+  if (M <= 32) {
+    const int64_t grid = cdiv(N, 64);
+    int8_row_gemv_kernel<<<dim3(static_cast<uint32_t>(grid)), dim3(kI8GemvThreads), 0, s>>>(
+        xb, ldx, static_cast<int>(M), static_cast<int>(K), q, scale, static_cast<int>(N), bb, yb, ldy);
+    return check_launch("int8_row_linear (gemv)");
+  }
+  GemmBatch batch{};
+  batch.count = 1;
+  batch.p[0] = GemmProblem{xb, qb, scale, bb, yb, nullptr, ldx, ldy, 0, static_cast<int>(M),
+                           static_cast<int>(K), static_cast<int>(N), static_cast<int>(N), 0, 0};
+  launch_gemm_default(batch, Code16{}, s, WCodec::kInt8Row);
+  return check_launch("int8_row_linear (gemm)");
 }
 
 extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx,

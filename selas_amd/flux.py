@@ -20,7 +20,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .codecs import EncodedTensor, encode_nf4, encode_raw
+from .codecs import EncodedTensor, encode_int8_row, encode_nf4, encode_raw
 from .kernels import FUSED, Kernels
 from .linear import UnitView, nf4_linear_grouped
 
@@ -213,19 +213,30 @@ class _Gen:
         return (self.pool[off: off + n] * std).view(*shape)
 
 
-def _linear_parts(gen: _Gen, name: str, n_in: int, n_out: int, dt, quant: bool, std: float = 0.02):
+def _linear_parts(gen: _Gen, name: str, n_in: int, n_out: int, dt, quant, std: float = 0.02):
+    """A linear's weight and bias; ``quant``: False (raw in dt), "nf4" or "int8" (int8_row), the choices
+    of selas's convert --quant (convert.py:170-187)."""
     out = {}
     w = gen.normal((n_out, n_in), std)
-    out[name + ".weight"] = encode_nf4(name + ".weight", w) if quant else encode_raw(name + ".weight", w, dt)
+    if quant == "int8":
+        out[name + ".weight"] = encode_int8_row(name + ".weight", w)
+    elif quant:
+        out[name + ".weight"] = encode_nf4(name + ".weight", w)
+    else:
+        out[name + ".weight"] = encode_raw(name + ".weight", w, dt)
     out[name + ".bias"] = encode_raw(name + ".bias", gen.normal((n_out,), std), dt)
     return out
 
 
 class RandomFlux:
-    """A FLUX-shaped transformer with random weights, NF4 blocks resident on one GPU."""
+    """A FLUX-shaped transformer with random weights, quantized blocks resident on one GPU.
+
+    ``quant``: "nf4" (default) or "int8" (int8_row) for the block and modulation linears."""
 
     def __init__(self, cfg: FluxConfig, device, dtype=torch.bfloat16, seed: int = 0, n_double=None, n_single=None,
-                 with_mods: bool = True):
+                 with_mods: bool = True, quant: str = "nf4"):
+        if quant not in ("nf4", "int8"):
+            raise ValueError(f"quant must be 'nf4' or 'int8', got {quant!r}")
         self.cfg, self.device, self.dt = cfg, torch.device(device), dtype
         nd = cfg.depth_double if n_double is None else n_double
         ns = cfg.depth_single if n_single is None else n_single
@@ -250,29 +261,29 @@ class RandomFlux:
         for _ in range(nd):
             t: dict[str, EncodedTensor] = {}
             for s in ("img", "txt"):
-                t.update(_linear_parts(gen, f"{s}_attn.qkv", d, 3 * d, dtype, True))
-                t.update(_linear_parts(gen, f"{s}_attn.proj", d, d, dtype, True))
-                t.update(_linear_parts(gen, f"{s}_mlp.0", d, m, dtype, True))
-                t.update(_linear_parts(gen, f"{s}_mlp.2", m, d, dtype, True))
+                t.update(_linear_parts(gen, f"{s}_attn.qkv", d, 3 * d, dtype, quant))
+                t.update(_linear_parts(gen, f"{s}_attn.proj", d, d, dtype, quant))
+                t.update(_linear_parts(gen, f"{s}_mlp.0", d, m, dtype, quant))
+                t.update(_linear_parts(gen, f"{s}_mlp.2", m, d, dtype, quant))
                 t.update(norms(f"{s}_attn.norm."))
             self.doubles.append(UnitView(t, dtype))
             if with_mods:
                 mt = {}
                 for s in ("img", "txt"):
-                    mt.update(_linear_parts(gen, f"{s}_mod.lin", d, 6 * d, dtype, True))
+                    mt.update(_linear_parts(gen, f"{s}_mod.lin", d, 6 * d, dtype, quant))
                 self.mods.append(UnitView(mt, dtype))
         for _ in range(ns):
-            t = _linear_parts(gen, "linear1", d, 3 * d + m, dtype, True)
-            t.update(_linear_parts(gen, "linear2", d + m, d, dtype, True))
+            t = _linear_parts(gen, "linear1", d, 3 * d + m, dtype, quant)
+            t.update(_linear_parts(gen, "linear2", d + m, d, dtype, quant))
             t.update(norms("norm."))
             self.singles.append(UnitView(t, dtype))
             if with_mods:
-                self.mods.append(UnitView(_linear_parts(gen, "modulation.lin", d, 3 * d, dtype, True), dtype))
+                self.mods.append(UnitView(_linear_parts(gen, "modulation.lin", d, 3 * d, dtype, quant), dtype))
         del gen
 
     def nf4_bytes(self) -> int:
         units = self.doubles + self.singles + self.mods
-        return sum(e.nbytes for u in units for e in u.tensors.values() if e.codec == "nf4")
+        return sum(e.nbytes for u in units for e in u.tensors.values() if e.codec in ("nf4", "int8_row"))
 
     def mod_prefixes(self) -> list[tuple[UnitView, str]]:
         nd = len(self.doubles)
@@ -287,7 +298,7 @@ class RandomFlux:
 
         ``grouped`` runs all modulation linears in one launch (same bits as one call per linear)."""
         pre = self.mod_prefixes()
-        if grouped:
+        if grouped and all(u.tensors[p + ".weight"].codec == "nf4" for u, p in pre):
             ws = []
             for u, p in pre:
                 e = u.tensors[p + ".weight"]

@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .codecs import EncodedTensor, decode, nf4_dequant
+from .codecs import EncodedTensor, decode, int8_row_dequant, nf4_dequant
 
 
 def _rows(x: torch.Tensor) -> torch.Tensor:
@@ -61,6 +61,62 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
         return F.linear(x, w, bias)
 
 
+def int8_row_linear(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, shape,
+                    bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(x, decode(W), bias)`` for an int8_row weight ``W`` of ``shape`` [N, K] (q int8 [N, K],
+    one fp32 scale per row). Outside the fused kernels the weight is decoded and a library GEMM runs."""
+    if len(shape) != 2:
+        raise ValueError(f"linear weight must be 2-D, got {tuple(shape)}")
+    n, k = int(shape[0]), int(shape[1])
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects {k}")
+    dev = _lib.require_gpu(x, q, scale, bias)
+    x2 = _rows(x)
+    m = x2.shape[0]
+    y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+    if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
+        bias = bias.to(x.dtype).contiguous()
+    try:
+        if x.dtype not in _lib.DTYPE_CODES:
+            raise _lib.Unsupported(f"dtype {x.dtype}")
+        with torch.cuda.device(dev):
+            _lib.call("selas_int8_row_linear", x2.data_ptr(), m, k, x2.stride(0), q.data_ptr(), scale.data_ptr(), n,
+                      _lib.ptr(bias), y.data_ptr(), n, _lib.dtype_code(x.dtype), _lib.stream(dev))
+        return y
+    except _lib.Unsupported:
+        return F.linear(x, int8_row_dequant(q, scale, x.dtype).view(n, k), bias)
+
+
+# Problems of the batched launches, per codec: (x, a, b, blocksize, code, shape, bias) with (a, b) =
+# (packed, absmax) for NF4 and (q, scale) for int8_row (blocksize and code then unused).
+def _single(codec: str, p) -> torch.Tensor:
+    x, a, b, bs, code, shape, bias = p
+    if codec == "nf4":
+        return nf4_linear(x, a, b, bs, code, shape, bias)
+    return int8_row_linear(x, a, b, shape, bias)
+
+
+def _launch_batched(codec: str, arr, count: int, code, dev) -> None:
+    with torch.cuda.device(dev):
+        if codec == "nf4":
+            _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), count, 64, _lib.code_array(code), _lib.BF16,
+                      _lib.stream(dev))
+        else:
+            _lib.call("selas_int8_row_linear_batched", ctypes.addressof(arr), count, _lib.BF16, _lib.stream(dev))
+
+
+def _batch_eligible(codec: str, problems):
+    """The common codebook of NF4 problems (None for int8_row); False when the batched launch cannot take them."""
+    if any(p[0].dtype != torch.bfloat16 for p in problems):
+        return False
+    if codec != "nf4":
+        return None
+    codes = {tuple(float(c) for c in p[4]) for p in problems}
+    if len(codes) != 1 or any(int(p[3]) != 64 for p in problems):
+        return False
+    return next(iter(codes))
+
+
 GROUPED_K = (1024, 2048, 3072)  # the grouped kernel keeps x in registers: K = 8 waves x 2, 4 or 6 blocks of 64
 GROUPED_MAX_M = 32
 GROUPED_MAX_WEIGHTS = 1023
@@ -76,20 +132,28 @@ def nf4_linear_batched(problems) -> list[torch.Tensor]:
     its own ``nf4_linear`` call; when any problem is outside the tiled GEMM (rows <= 32,
     unsupported shapes) they run one by one.
     """
-    problems = list(problems)
+    return _batched("nf4", list(problems))
+
+
+def int8_row_linear_batched(problems) -> list[torch.Tensor]:
+    """``[int8_row_linear(*p) for p in problems]`` with the tiled GEMMs in one launch; ``problems`` are
+    (x, q, scale, shape, bias) tuples. As ``nf4_linear_batched`` otherwise."""
+    return _batched("int8_row", [(x, q, s, None, None, shape, b) for x, q, s, shape, b in problems])
+
+
+def _batched(codec: str, problems):
     if len(problems) <= 1:
-        return [nf4_linear(*p) for p in problems]
+        return [_single(codec, p) for p in problems]
     outs = []
     for i in range(0, len(problems), _lib.MAX_BATCHED_LINEARS):
-        outs += _batched_chunk(problems[i:i + _lib.MAX_BATCHED_LINEARS])
+        outs += _batched_chunk(codec, problems[i:i + _lib.MAX_BATCHED_LINEARS])
     return outs
 
 
-def _batched_chunk(problems):
-    codes = {tuple(float(c) for c in p[4]) for p in problems}
-    x0 = problems[0][0]
-    if len(codes) != 1 or any(p[0].dtype != torch.bfloat16 or int(p[3]) != 64 for p in problems):
-        return [nf4_linear(*p) for p in problems]
+def _batched_chunk(codec: str, problems):
+    code = _batch_eligible(codec, problems)
+    if code is False:
+        return [_single(codec, p) for p in problems]
     dev = _lib.require_gpu(*(p[0] for p in problems), *(p[1] for p in problems))
     arr = (_lib.GemmProblem * len(problems))()
     outs, keep = [], []
@@ -106,11 +170,9 @@ def _batched_chunk(problems):
         arr[i] = _lib.GemmProblem(x2.data_ptr(), x2.shape[0], k, x2.stride(0), packed.data_ptr(), absmax.data_ptr(), n,
                                   _lib.ptr(bias), y.data_ptr(), n)
     try:
-        with torch.cuda.device(dev):
-            _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), len(problems), 64,
-                      _lib.code_array(next(iter(codes))), _lib.BF16, _lib.stream(dev))
+        _launch_batched(codec, arr, len(problems), code, dev)
     except _lib.Unsupported:
-        return [nf4_linear(*p) for p in problems]
+        return [_single(codec, p) for p in problems]
     del keep  # the launch is queued on the stream that later reuses this memory
     return outs
 
@@ -126,18 +188,26 @@ def nf4_linear_gelu(problems) -> list[torch.Tensor | None]:
     take a problem (rows <= 32, N - gelu_cols not a multiple of 256, shapes outside the tiled GEMM), that
     composition runs instead.
     """
-    problems = list(problems)
+    return _gelu("nf4", list(problems))
+
+
+def int8_row_linear_gelu(problems) -> list:
+    """``nf4_linear_gelu`` for int8_row weights: (x, q, scale, shape, bias, gelu_cols, gelu_out) tuples."""
+    return _gelu("int8_row", [(x, q, s, None, None, shape, b, gc, out) for x, q, s, shape, b, gc, out in problems])
+
+
+def _gelu(codec: str, problems):
     outs = []
     for i in range(0, len(problems), _lib.MAX_BATCHED_LINEARS):
-        outs += _gelu_chunk(problems[i:i + _lib.MAX_BATCHED_LINEARS])
+        outs += _gelu_chunk(codec, problems[i:i + _lib.MAX_BATCHED_LINEARS])
     return outs
 
 
-def _gelu_composed(x, packed, absmax, blocksize, code, shape, bias, gelu_cols, gelu_out):
+def _gelu_composed(codec, x, a, b, blocksize, code, shape, bias, gelu_cols, gelu_out):
     from .kernels import Kernels
 
     n = int(shape[0])
-    y = nf4_linear(x, packed, absmax, blocksize, code, shape, bias)
+    y = _single(codec, (x, a, b, blocksize, code, shape, bias))
     g = Kernels().gelu(y[..., n - gelu_cols:])
     if gelu_out is None:
         gelu_out = g
@@ -146,10 +216,10 @@ def _gelu_composed(x, packed, absmax, blocksize, code, shape, bias, gelu_cols, g
     return (y[..., :n - gelu_cols].contiguous() if gelu_cols < n else None), gelu_out
 
 
-def _gelu_chunk(problems):
-    codes = {tuple(float(c) for c in p[4]) for p in problems}
-    if len(codes) != 1 or any(p[0].dtype != torch.bfloat16 or int(p[3]) != 64 for p in problems):
-        return [_gelu_composed(*p) for p in problems]
+def _gelu_chunk(codec: str, problems):
+    code = _batch_eligible(codec, problems)
+    if code is False:
+        return [_gelu_composed(codec, *p) for p in problems]
     dev = _lib.require_gpu(*(p[0] for p in problems), *(p[1] for p in problems))
     arr = (_lib.GemmProblem * len(problems))()
     outs, keep = [], []
@@ -183,11 +253,9 @@ def _gelu_chunk(problems):
         arr[i] = _lib.GemmProblem(x2.data_ptr(), x2.shape[0], k, x2.stride(0), packed.data_ptr(), absmax.data_ptr(), n,
                                   _lib.ptr(bias), _lib.ptr(y), n - gc, gelu_out.data_ptr(), ldg, gc)
     try:
-        with torch.cuda.device(dev):
-            _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), len(problems), 64,
-                      _lib.code_array(next(iter(codes))), _lib.BF16, _lib.stream(dev))
+        _launch_batched(codec, arr, len(problems), code, dev)
     except _lib.Unsupported:
-        return [_gelu_composed(*p[:8], o) for p, (_, o) in zip(problems, outs)]
+        return [_gelu_composed(codec, *p[:8], o) for p, (_, o) in zip(problems, outs)]
     del keep
     return outs
 
@@ -307,34 +375,42 @@ class UnitView:
             self._views[key] = out
         return out
 
+    def _problem(self, x: torch.Tensor, prefix: str, dtype: torch.dtype):
+        """(codec, (x, a, b, blocksize, code, shape, bias)) for a fused codec, or (None, bias)."""
+        e = self.tensors[prefix + ".weight"]
+        bname = prefix + ".bias"
+        b = self.get(bname, dtype) if bname in self.tensors else None
+        if x.dtype != dtype or len(e.shape) != 2:
+            return None, b
+        if e.codec == "nf4":
+            return "nf4", (x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"], e.shape, b)
+        if e.codec == "int8_row":
+            return "int8_row", (x, e.parts["q"], e.parts["scale"], None, None, e.shape, b)
+        return None, b
+
     def linear_many(self, items, dtype: torch.dtype | None = None) -> list[torch.Tensor]:
-        """``[self.linear(x, prefix) for x, prefix in items]``, NF4 tiled GEMMs in one launch."""
+        """``[self.linear(x, prefix) for x, prefix in items]``, the tiled GEMMs of one codec in one launch."""
         dtype = dtype or self.dtype
         items = list(items)
-        probs = []
-        for x, prefix in items:
-            e = self.tensors[prefix + ".weight"]
-            if e.codec != "nf4" or x.dtype != dtype:
-                return [self.linear(x, p, dtype) for x, p in items]
-            bname = prefix + ".bias"
-            b = self.get(bname, dtype) if bname in self.tensors else None
-            probs.append((x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"], e.shape, b))
-        return nf4_linear_batched(probs)
+        probs = [self._problem(x, prefix, dtype) for x, prefix in items]
+        codecs = {c for c, _ in probs}
+        if len(codecs) != 1 or None in codecs:
+            return [self.linear(x, p, dtype) for x, p in items]
+        return _batched(codecs.pop(), [p for _, p in probs])
 
     def linear_gelu_many(self, items, dtype: torch.dtype | None = None) -> list:
-        """For (x, prefix, gelu_cols, gelu_out) items: ``nf4_linear_gelu`` of the unit's weights (the NF4 ones in one
-        launch); returns (plain columns or None, gelu_out) per item."""
+        """For (x, prefix, gelu_cols, gelu_out) items: the linear with GELU applied to its last gelu_cols
+        output columns, written to gelu_out (NF4 and int8_row weights: in the GEMM epilogue, one launch per
+        codec); returns (plain columns or None, gelu_out) per item."""
         dtype = dtype or self.dtype
-        fused, results = [], []
-        for x, prefix, gc, out in items:
-            e = self.tensors[prefix + ".weight"]
-            bname = prefix + ".bias"
-            b = self.get(bname, dtype) if bname in self.tensors else None
-            if e.codec == "nf4" and x.dtype == dtype:
-                fused.append((x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"],
-                              e.shape, b, gc, out))
+        by_codec: dict[str, list] = {}
+        results: list = []
+        for i, (x, prefix, gc, out) in enumerate(items):
+            codec, prob = self._problem(x, prefix, dtype)
+            if codec is not None:
+                by_codec.setdefault(codec, []).append((i, prob + (gc, out)))
                 results.append(None)
-            else:  # raw weights: the linear, then the GELU segment
+            else:  # other weights: the linear, then the GELU segment
                 from .kernels import Kernels
 
                 y = self.linear(x, prefix, dtype)
@@ -343,15 +419,14 @@ class UnitView:
                 if out is not None:
                     out.copy_(g)
                 results.append((y[..., :n - gc].contiguous() if gc < n else None, out if out is not None else g))
-        done = iter(nf4_linear_gelu(fused))
-        return [next(done) if r is None else r for r in results]
+        for codec, group in by_codec.items():
+            for (i, _), r in zip(group, _gelu(codec, [p for _, p in group])):
+                results[i] = r
+        return results
 
     def linear(self, x: torch.Tensor, prefix: str, dtype: torch.dtype | None = None) -> torch.Tensor:
         dtype = dtype or self.dtype
-        e = self.tensors[prefix + ".weight"]
-        bname = prefix + ".bias"
-        b = self.get(bname, dtype) if bname in self.tensors else None
-        if e.codec == "nf4" and x.dtype == dtype:
-            return nf4_linear(x, e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"],
-                              e.shape, b)
-        return F.linear(x, self.get(prefix + ".weight", dtype), b)
+        codec, prob = self._problem(x, prefix, dtype)
+        if codec is not None:
+            return _single(codec, prob)
+        return F.linear(x, self.get(prefix + ".weight", dtype), prob)

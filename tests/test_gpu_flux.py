@@ -144,3 +144,32 @@ def test_fused_gelu_blocks_equal_composed_blocks(model, monkeypatch):
     composed = run()
     for a, b in zip(fused, composed):
         assert torch.equal(a, b)
+
+
+def test_int8_row_blocks(monkeypatch):
+    # The same blocks with int8_row weights (selas convert --quant int8): fused int8 GEMMs, GELU
+    # epilogue and skinny modulation linears, against the oracle decoding the same q and scales.
+    m8 = F.RandomFlux(CFG, "cuda", torch.bfloat16, seed=5, n_double=1, n_single=1, quant="int8")
+    assert m8.doubles[0].codec("img_mlp.0.weight") == "int8_row"
+    dev = torch.device("cuda")
+    img, txt, cos, sin = inputs(2, 64, 8)
+    mod = (torch.randn(2, 12 * CFG.hidden, generator=seeded(30)) * 0.3).to(torch.bfloat16)
+    gi, gt = F.double_block(m8.doubles[0], img.to(dev), txt.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG,
+                            torch.bfloat16, False)
+    ri, rt = OF.double_block(oracle_unit(m8.doubles[0]), img, txt, mod.float(), cos, sin, OCFG, torch.float32, False)
+    assert rel(gi - img.cuda(), ri - img) < 2e-2 and rel(gt - txt.cuda(), rt - txt) < 2e-2
+    x = torch.cat((txt, img), dim=1)
+    smod = (torch.randn(2, 3 * CFG.hidden, generator=seeded(31)) * 0.3).to(torch.bfloat16)
+    gx = F.single_block(m8.singles[0], x.to(dev), smod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16, False)
+    rx = OF.single_block(oracle_unit(m8.singles[0]), x, smod.float(), cos, sin, OCFG, torch.float32, False)
+    assert rel(gx - x.cuda(), rx - x) < 2e-2 and rel(gx, rx) < 4e-3
+    sv = torch.nn.functional.silu(torch.randn(5, 1, CFG.hidden, generator=seeded(32))).to(torch.bfloat16)
+    mods = m8.modulations(sv.to(dev))
+    u = oracle_unit(m8.mods[1])
+    assert rel(mods[1], u.linear(sv.float(), "modulation.lin")) < 4e-3
+    fused = F.single_block(m8.singles[0], x.to(dev), smod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
+                           False)
+    monkeypatch.setattr(F, "_fused_gelu", lambda w, k: False)
+    composed = F.single_block(m8.singles[0], x.to(dev), smod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
+                              False)
+    assert torch.equal(fused, composed)

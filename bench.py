@@ -255,6 +255,88 @@ def bench_modulations(dev, steps, warmup):
             "grouped_call_ms": call, "per_linear_kernel_ms_mean": per, "gbs_per_linear": nbytes / (per * 76) / 1e6}
 
 
+def bench_int8_row(dev, steps, warmup, copies=8):
+    """int8_row weights (selas convert --quant int8): the single block's linears at 1024^2 (tiled GEMM with
+    the int8 operand), the same through decode + F.linear, and the 76 modulation linears at M = 28 (skinny
+    kernel, one launch per linear; 3.2 GB of int8 weights)."""
+    from selas_amd import codecs
+    from selas_amd.linear import int8_row_linear
+
+    def weight(n, k, seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        return codecs.encode_int8_row("w", torch.randn(n, k, generator=g, device=dev) * 0.02)
+
+    def run(x, e, b=None):
+        return int8_row_linear(x, e.parts["q"], e.parts["scale"], e.shape, b)
+
+    f1 = 2.0 * M_1024 * (3 * D + MLP) * D
+    f2 = 2.0 * M_1024 * D * (D + MLP)
+    w1 = [weight(3 * D + MLP, D, 700 + i) for i in range(copies)]
+    w2 = [weight(D, D + MLP, 800 + i) for i in range(copies)]
+    b1, b2 = bias(3 * D + MLP, 1, dev), bias(D, 2, dev)
+    x1, x2 = act(M_1024, D, 2, dev), act(M_1024, D + MLP, 3, dev)
+    for i in range(warmup):
+        run(x1, w1[i % copies], b1)
+        run(x2, w2[i % copies], b2)
+    torch.cuda.synchronize(dev)
+    tm = Timer()
+    for i in range(steps):
+        t = tm.start("linear1")
+        run(x1, w1[i % copies], b1)
+        tm.stop(t)
+        t = tm.start("linear2")
+        run(x2, w2[i % copies], b2)
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
+    k1, k2 = tm.mean_ms("linear1"), tm.mean_ms("linear2")
+    for i in range(max(3, steps // 5)):
+        t = tm.start("library")
+        torch.nn.functional.linear(x1, codecs.decode("int8_row", w1[i % copies].parts, {}, w1[0].shape,
+                                                     torch.bfloat16), b1)
+        torch.nn.functional.linear(x2, codecs.decode("int8_row", w2[i % copies].parts, {}, w2[0].shape,
+                                                     torch.bfloat16), b2)
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
+    lib_ms = tm.median_ms("library")
+    del w1, w2
+    s = 28
+    ws = [weight(6 * D, D, 900 + i) for i in range(38)] + [weight(3 * D, D, 1000 + i) for i in range(38)]
+    bs = [bias(e.shape[0], 1100 + i, dev) for i, e in enumerate(ws)]
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.nn.functional.silu(torch.randn(s, D, generator=g, device=dev)).to(torch.bfloat16)
+    nbytes = sum(e.nbytes for e in ws) + sum(b.numel() * 2 for b in bs) + s * D * 2 + sum(s * e.shape[0] * 2 for e in ws)
+    # The 76 launches straight through the C ABI (preallocated outputs), timed as one batch: the
+    # Python wrapper's own time per call is about that of the kernel and would leave the GPU idle.
+    from selas_amd import _lib
+
+    lib, st = _lib.load(), _lib.stream(dev)
+    ys = [torch.empty(s, e.shape[0], dtype=torch.bfloat16, device=dev) for e in ws]
+    args = [(x.data_ptr(), s, D, D, e.parts["q"].data_ptr(), e.parts["scale"].data_ptr(), e.shape[0], b.data_ptr(),
+             y.data_ptr(), e.shape[0], _lib.BF16, st) for e, b, y in zip(ws, bs, ys)]
+    f = lib.selas_int8_row_linear
+    for _ in range(max(2, warmup // 10)):
+        for a in args:
+            f(*a)
+    torch.cuda.synchronize(dev)
+    reps = 5
+    t = tm.start("gemv")
+    for _ in range(reps):
+        for a in args:
+            f(*a)
+    tm.stop(t)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(ys[0], run(x, ws[0], bs[0]))
+    per = tm.mean_ms("gemv") / (reps * len(args))
+    return {
+        "block_linears": {"kernel_ms": {"linear1": k1, "linear2": k2},
+                          "kernel_tflops": {"linear1": f1 / k1 / 1e9, "linear2": f2 / k2 / 1e9},
+                          "achieved_tflops": (f1 + f2) / (k1 + k2) / 1e9,
+                          "library_path_ms": lib_ms, "library_path_tflops": (f1 + f2) / lib_ms / 1e9},
+        "modulations_m28": {"launches": 76, "bytes": nbytes, "kernel_ms_mean": per, "total_ms": per * 76,
+                            "gbs": nbytes / (per * 76) / 1e6, "frac_hbm": nbytes / (per * 76) / 1e6 / PEAK_HBM_GBS},
+    }
+
+
 def bench_segments(dev, steps, warmup):
     from selas_amd.kernels import Kernels
 
@@ -516,6 +598,10 @@ def main():
         extra["library_path"] = bench_library_path(dev, a.steps, a.warmup)
         log(f"bench: library path {extra['library_path']['tflops']:.1f} TFLOP/s")
         extra["attention"] = bench_attention(dev, a.steps, a.warmup)
+        extra["int8_row"] = bench_int8_row(dev, a.steps, a.warmup)
+        i8 = extra["int8_row"]
+        log(f"bench: int8_row block linears {i8['block_linears']['achieved_tflops']:.1f} TFLOP/s, "
+            f"modulations {i8['modulations_m28']['gbs']:.0f} GB/s")
         log("bench: attention " + ", ".join(f"{k}: fused {v['kernel']['tflops']:.0f} / SDPA {v['sdpa']['tflops']:.0f} TFLOP/s"
                                             for k, v in extra["attention"].items()))
     if not a.no_full_step:

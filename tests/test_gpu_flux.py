@@ -173,3 +173,11 @@ def test_int8_row_blocks(monkeypatch):
     composed = F.single_block(m8.singles[0], x.to(dev), smod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
                               False)
     assert torch.equal(fused, composed)
+
+
+def test_planner_measurements(dev):
+    from selas_amd import planner as P
+
+    prof = P.measure_profile(dev)
+    assert prof.measured == ("attn_flops", "dequant_bw", "matmul_flops")
+    assert 2e14 < prof.matmul_flops < 2.5e15 and 2e14 < prof.attn_flops < 2.5e15 and 2e11 < prof.dequant_bw < 8e12

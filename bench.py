@@ -327,13 +327,31 @@ def bench_int8_row(dev, steps, warmup, copies=8):
     torch.cuda.synchronize(dev)
     assert torch.equal(ys[0], run(x, ws[0], bs[0]))
     per = tm.mean_ms("gemv") / (reps * len(args))
+    # All 76 in one launch of the streaming kernel.
+    from selas_amd.linear import GroupedPlan
+
+    plan = GroupedPlan([(e.parts["q"], e.parts["scale"], None, None, e.shape, b) for e, b in zip(ws, bs)], s, dev,
+                       codec="int8_row")
+    assert plan.supported
+    for _ in range(max(2, warmup // 10)):
+        plan.run(x)
+    torch.cuda.synchronize(dev)
+    for _ in range(max(5, steps)):
+        t = tm.start("grouped")
+        plan.run(x)
+        tm.stop(t)
+    torch.cuda.synchronize(dev)
+    grp = tm.median_ms("grouped")
+    assert all(torch.equal(a, b) for a, b in zip(plan.outs, ys))
     return {
         "block_linears": {"kernel_ms": {"linear1": k1, "linear2": k2},
                           "kernel_tflops": {"linear1": f1 / k1 / 1e9, "linear2": f2 / k2 / 1e9},
                           "achieved_tflops": (f1 + f2) / (k1 + k2) / 1e9,
                           "library_path_ms": lib_ms, "library_path_tflops": (f1 + f2) / lib_ms / 1e9},
-        "modulations_m28": {"launches": 76, "bytes": nbytes, "kernel_ms_mean": per, "total_ms": per * 76,
-                            "gbs": nbytes / (per * 76) / 1e6, "frac_hbm": nbytes / (per * 76) / 1e6 / PEAK_HBM_GBS},
+        "modulations_m28": {"launches": 76, "bytes": nbytes, "grouped_kernel_ms": grp, "gbs_grouped": nbytes / grp / 1e6,
+                            "frac_hbm_grouped": nbytes / grp / 1e6 / PEAK_HBM_GBS,
+                            "per_linear_kernel_ms_mean": per, "per_linear_total_ms": per * 76,
+                            "gbs_per_linear": nbytes / (per * 76) / 1e6},
     }
 
 
@@ -601,7 +619,8 @@ def main():
         extra["int8_row"] = bench_int8_row(dev, a.steps, a.warmup)
         i8 = extra["int8_row"]
         log(f"bench: int8_row block linears {i8['block_linears']['achieved_tflops']:.1f} TFLOP/s, "
-            f"modulations {i8['modulations_m28']['gbs']:.0f} GB/s")
+            f"modulations grouped {i8['modulations_m28']['gbs_grouped']:.0f} GB/s, "
+            f"per-linear {i8['modulations_m28']['gbs_per_linear']:.0f} GB/s")
         log("bench: attention " + ", ".join(f"{k}: fused {v['kernel']['tflops']:.0f} / SDPA {v['sdpa']['tflops']:.0f} TFLOP/s"
                                             for k, v in extra["attention"].items()))
     if not a.no_full_step:

@@ -161,7 +161,8 @@ int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t cou
  * dtype as for selas_nf4_linear.
  * M > 32 runs the tiled MFMA GEMM of selas_nf4_linear with the int8 operand
  * bf16(q * bf16(scale)), the reference's decoded weight bit for bit. M <= 32
- * runs a skinny kernel that multiplies x by q exactly and scales the fp32 row
+ * runs a skinny kernel (for K = 1024, 2048, 3072 the streaming kernel of
+ * selas_int8_row_linear_grouped) that multiplies x by q exactly and scales the fp32 row
  * sums by bf16(scale): it agrees with the decoded-weight product to the bf16
  * rounding of the decoded weight. Returns SELAS_EUNSUPPORTED for K % 64 != 0,
  * misaligned rows or a dtype other than bf16 (the caller then decodes with
@@ -178,6 +179,7 @@ int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_t ldx, cons
  * No counterpart in the reference (see selas_nf4_linear_batched).
  */
 int selas_int8_row_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int dtype, void *stream);
+
 
 /*
  * One NF4 weight of a grouped skinny linear (device-memory array element).
@@ -207,6 +209,17 @@ typedef struct selas_nf4_gemv_desc {
 int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx, const selas_nf4_gemv_desc *descs,
                              int64_t count, int64_t total_n, int64_t blocksize, const float code[16], int dtype,
                              void *stream);
+
+/*
+ * selas_nf4_linear_grouped for int8_row weights (M <= 32, K = 1024, 2048 or
+ * 3072, bf16): in each descriptor `packed` holds q [n, K] (16-byte aligned) and
+ * `absmax` the n row scales. Each output has the bits selas_int8_row_linear
+ * gives for that weight alone (the same kernel serves M <= 32 there).
+ * Replaces the per-weight UnitView.linear calls of FluxRunner.modulations
+ * (selas/models/flux.py:428-445) for int8_row weights.
+ */
+int selas_int8_row_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx, const selas_nf4_gemv_desc *descs,
+                                  int64_t count, int64_t total_n, int dtype, void *stream);
 
 /* ------------------------------------------------------------ segments
  *

@@ -34,6 +34,7 @@ SIGNATURES: dict[str, list] = {
     "selas_int8_row_encode": [_P, _I64, _I64, _P, _P, _P],
     "selas_int8_row_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _INT, _P],
     "selas_int8_row_linear_batched": [_P, _I64, _INT, _P],
+    "selas_int8_row_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _INT, _P],
     "selas_mod_in": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _INT, _P],
     "selas_gated_add": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P],
     "selas_gated_add_mod": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P, _I64,

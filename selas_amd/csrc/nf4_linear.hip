@@ -662,6 +662,209 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   finish((u_end - 1 - u_begin) & (L::kRedBufs - 1), d_prev, row_prev, bias_prev);
 }
 
+// ------------------------------------------------------- int8_row streaming skinny GEMM
+//
+// For M <= 32, K = 1024, 2048, 3072 and int8_row weights: the structure of
+// nf4_gemv_stream (persistent workgroups of NW waves over 32-row units of one
+// or many weights, wave w owning the K blocks [w*BPW, (w+1)*BPW), each wave's
+// slice of a unit's rows copied HBM -> LDS by whole-line DMA, XOR-swizzled so
+// that the MFMA-order reads are conflict-free, partial sums added in LDS in
+// wave order) with the operand of int8_row_gemv_kernel: x stays bf16 in
+// registers for the whole launch, the biased byte u = q + 128 converts exactly
+// to bf16, sum_k x q = sum_k x u - 128 sum_k x (the second sum computed once,
+// per wave, against ones), and the fp32 row sums are scaled by bf16(scale).
+template <int NW, int BPW>
+struct I8Layout {
+  static constexpr int kThreads = 64 * NW;
+  static constexpr int kChunks = 4 * BPW;        // 16-byte chunks of a row's slice (64 * BPW bytes)
+  static constexpr int kCodeInstrs = 2 * BPW;    // 32 rows x kChunks chunks / 64 lanes
+  static constexpr int kCodeBytes = kSgRows * kChunks * 16;
+  static constexpr int kRedBufs = NW == 4 ? 2 : 1;
+  static constexpr int kRedBytes = kRedBufs * NW * 16 * 64 * 4;
+  static constexpr int kRed = NW * kCodeBytes;   // byte offsets in dynamic LDS; the stages start at 0
+  static constexpr int kPrefix = kRed + kRedBytes;
+  static constexpr int kMaxBytes = kPrefix + (kSgMaxDescs + 1) * 4;
+  static constexpr int kOuts = 1024 / kThreads;
+  static_assert(kChunks % 8 == 0, "the swizzle permutes chunks within aligned groups of 8");
+  static_assert(kMaxBytes <= 160 * 1024, "LDS");
+};
+
+template <int NW, int BPW>
+__global__ __launch_bounds__(64 * NW, 1) void int8_gemv_stream(
+    const uint16_t *__restrict__ x, int64_t ldx, int M, const GemvDesc *__restrict__ descs, int count,
+    GemvDesc one) {
+  using L = I8Layout<NW, BPW>;
+  constexpr int kblocks = L::kThreads / 64 * BPW, row_bytes = 64 * kblocks, kThreads = L::kThreads;
+  extern __shared__ __align__(16) uint32_t lds_words[];
+  uint8_t *lds = reinterpret_cast<uint8_t *>(lds_words);
+  int *prefix = reinterpret_cast<int *>(lds + L::kPrefix);
+  float *red = reinterpret_cast<float *>(lds + L::kRed);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, c = lane & 31;
+
+  if (wave == 0) {
+    // prefix[g] = units (32-row slabs) before weight g: a wave-wide scan, 64 weights at a time.
+    int carry = 0;
+    for (int base = 0; base < count; base += 64) {
+      const int g = base + lane;
+      int v = 0;
+      if (g < count) v = static_cast<int>(((descs ? descs[g].n : one.n) + kSgRows - 1) / kSgRows);
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(v, off);
+        if (lane >= off) v += t;
+      }
+      if (g < count) prefix[g + 1] = carry + v;
+      carry += __shfl(v, 63);
+    }
+    if (lane == 0) prefix[0] = 0;
+  }
+
+  // x fragments of this wave's slice (block b, sub-step s: k = 64*(kb0+b) + 32h + 8s .. +8; rows
+  // past M repeat row M-1) and the slice's sum_k x per row, against ones.
+  const int kb0 = wave * BPW;
+  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 64 * kb0 + 32 * h;
+  bf16x8 xf[BPW][4];
+#pragma unroll
+  for (int b = 0; b < BPW; ++b)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xf[b][s] = *reinterpret_cast<const bf16x8 *>(xr + 64 * b + 8 * s);
+  const uint32_t one2 = 0x3F803F80u;
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(one2, one2, one2, one2));
+  f32x16 accx = f32x16{};
+#pragma unroll
+  for (int b = 0; b < BPW; ++b)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) accx = mfma32(xf[b][s], ones, accx);
+
+  uint8_t *stage = lds + wave * L::kCodeBytes;
+  // MFMA-order reads: lane (c, h) takes chunks 4b + 2h and 4b + 2h + 1 of row c.
+  const int rd_base = c * L::kChunks * 16, rd_swz = sg_swz<L::kChunks>(c);
+  __syncthreads();  // prefix ready
+
+  const int units_total = prefix[count];
+  const int units_per_wg = (units_total + gridDim.x - 1) / gridDim.x;
+  const int u_begin = blockIdx.x * units_per_wg;
+  const int u_end = min(u_begin + units_per_wg, units_total);
+  if (u_begin >= u_end) return;  // uniform over the workgroup
+
+  auto locate = [&](int u, int g) {
+    while (prefix[g + 1] <= u) ++g;
+    return __builtin_amdgcn_readfirstlane(g);
+  };
+  auto desc = [&](int g) { return uniform_desc(descs ? descs[g] : one); };
+  // Code instruction j fetches chunk (p ^ swz(r)) of row r into stage slot 64j + lane = r*kChunks + p.
+  // The buffer starts at the unit's first row, so rows past the weight's end read as 0.
+  auto issue = [&](const SDesc &d, int row0) {
+    const auto rc = make_rsrc(d.packed + static_cast<int64_t>(row0) * row_bytes,
+                              static_cast<uint32_t>(max(d.n - row0, 0)) * row_bytes);
+#pragma unroll
+    for (int j = 0; j < L::kCodeInstrs; ++j) {
+      const uint32_t q = 64u * j + lane, r = q / L::kChunks, p = q - r * L::kChunks;
+      load_lds16_at(rc, stage + 1024 * j, r * row_bytes + 64 * kb0 + 16 * (p ^ sg_swz<L::kChunks>(r)));
+    }
+  };
+  // Bias bits and row scale of the output column this thread stores (loaded one unit ahead,
+  // through buffer resources: a flat access could make LDS reads wait for the stage DMA).
+  auto load_col = [&](const SDesc &d, int row0, uint32_t &bias_bits, float &scale) {
+    const int n = min(row0 + c, d.n - 1);
+    bias_bits = 0u;
+    if (d.bias)
+      bias_bits = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(d.bias, static_cast<uint32_t>(d.n * 2)),
+                                                       static_cast<uint32_t>(n) * 2u, 0, 0);
+    scale = load_f32(make_rsrc(d.absmax, static_cast<uint32_t>(d.n * 4)), static_cast<uint32_t>(n) * 4u, 0);
+  };
+  auto finish = [&](int buf, const SDesc &d, int row0, uint32_t bias_bits, float scale) {
+    const int N = d.n;
+    const float bv = bf16_bits_to_f32(static_cast<uint16_t>(bias_bits));
+    const float sb = bf16_bits_to_f32(bf16_bits_rne(scale));
+    const auto ry = make_rsrc(d.y, static_cast<uint32_t>(((M - 1) * d.ldy + N) * 2));
+    const float *rb = red + buf * NW * 1024;
+#pragma unroll
+    for (int i = 0; i < L::kOuts; ++i) {
+      const int e = tid + kThreads * i;
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v += rb[w * 1024 + e];
+      const int r = e >> 6;
+      const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+      const int n = row0 + c;
+      if (m < M && n < N)
+        __builtin_amdgcn_raw_buffer_store_b16(bf16_bits_rne(sb * v + bv), ry,
+                                              static_cast<uint32_t>(m * d.ldy + n) * 2u, 0, 0);
+    }
+  };
+  uint4 cw[BPW][2];
+  auto read_stage = [&]() {
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        cw[b][t] = *reinterpret_cast<const uint4 *>(stage + rd_base + 16 * ((4 * b + 2 * h + t) ^ rd_swz));
+  };
+
+  int g_cur = locate(u_begin, 0);
+  SDesc d_cur = desc(g_cur);
+  int row_cur = (u_begin - prefix[g_cur]) * kSgRows;
+  issue(d_cur, row_cur);
+  wait_vmcnt<0>();
+  __syncthreads();  // the first unit's rows are in LDS
+  read_stage();
+  SDesc d_prev = d_cur;
+  int row_prev = row_cur;
+  uint32_t bias_prev = 0;
+  float scale_prev = 0.0f;
+  for (int u = u_begin; u < u_end; ++u) {
+    const int buf = (u - u_begin) & (L::kRedBufs - 1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage read before the next DMA overwrites it
+    uint32_t bias_cur;
+    float scale_cur;
+    load_col(d_cur, row_cur, bias_cur, scale_cur);
+    int g_nxt = g_cur, row_nxt = row_cur + kSgRows;
+    SDesc d_nxt = d_cur;
+    const bool more = u + 1 < u_end;
+    if (more && row_nxt >= d_cur.n) {
+      g_nxt = locate(u + 1, g_cur);
+      d_nxt = desc(g_nxt);
+      row_nxt = (u + 1 - prefix[g_nxt]) * kSgRows;
+    }
+    if (u > u_begin) finish(buf ^ (L::kRedBufs - 1), d_prev, row_prev, bias_prev, scale_prev);  // unit u-1
+    if (more) issue(d_nxt, row_nxt);
+
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 &w = cw[b][s >> 1];
+        acc = mfma32(xf[b][s], biased_i8_to_bf16((s & 1) ? w.z : w.x, (s & 1) ? w.w : w.y), acc);
+      }
+    wait_vmcnt<0>();  // this wave's DMAs of unit u+1 have landed
+    float *rw = red + buf * NW * 1024;
+    if constexpr (L::kRedBufs == 1) {
+      __syncthreads();  // every wave has summed unit u-1 from the single buffer
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r] - 128.0f * accx[r];
+      if (more) read_stage();  // its latency overlaps the barrier
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r] - 128.0f * accx[r];
+      __syncthreads();  // partials of unit u complete; every wave's DMAs of unit u+1 landed
+      if (more) read_stage();
+    }
+    d_prev = d_cur;
+    row_prev = row_cur;
+    bias_prev = bias_cur;
+    scale_prev = scale_cur;
+    g_cur = g_nxt;
+    d_cur = d_nxt;
+    row_cur = row_nxt;
+  }
+  finish((u_end - 1 - u_begin) & (L::kRedBufs - 1), d_prev, row_prev, bias_prev, scale_prev);
+}
+
 int cu_count() {
   static int n = [] {
     int dev = 0, v = 0;
@@ -701,6 +904,35 @@ int launch_gemv_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, con
     case 2048: return launch_stream<NW, 2048 / 64 / NW>(x, ldx, M, descs, count, one, total_n, c, s);
     case 3072: return launch_stream<NW, 3072 / 64 / NW>(x, ldx, M, descs, count, one, total_n, c, s);
     default: return set_error(SELAS_EUNSUPPORTED, "nf4_linear: streaming skinny kernel takes K = 1024, 2048, 3072");
+  }
+}
+
+template <int NW, int BPW>
+int launch_i8_stream(const uint16_t *x, int64_t ldx, int64_t M, const GemvDesc *descs, int count,
+                     const GemvDesc &one, int64_t total_n, hipStream_t s) {
+  using L = I8Layout<NW, BPW>;
+  const int64_t units = cdiv(total_n, kSgRows) + count;
+  const int64_t grid = min(units, static_cast<int64_t>(cu_count()));
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&int8_gemv_stream<NW, BPW>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, L::kMaxBytes);
+  if (attr != hipSuccess)
+    return set_error(SELAS_EHIP, "int8_row_linear: cannot reserve %d bytes of LDS: %s", L::kMaxBytes,
+                     hipGetErrorString(attr));
+  const size_t lds = L::kPrefix + (count + 1) * sizeof(int);
+  int8_gemv_stream<NW, BPW><<<dim3(static_cast<uint32_t>(grid)), dim3(L::kThreads), lds, s>>>(
+      x, ldx, static_cast<int>(M), descs, count, one);
+  return check_launch("int8_row_linear (streaming skinny gemm)");
+}
+
+int launch_i8_gemv_stream(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, const GemvDesc *descs, int count,
+                          const GemvDesc &one, int64_t total_n, hipStream_t s) {
+  constexpr int NW = 8;
+  switch (K) {
+    case 1024: return launch_i8_stream<NW, 1024 / 64 / NW>(x, ldx, M, descs, count, one, total_n, s);
+    case 2048: return launch_i8_stream<NW, 2048 / 64 / NW>(x, ldx, M, descs, count, one, total_n, s);
+    case 3072: return launch_i8_stream<NW, 3072 / 64 / NW>(x, ldx, M, descs, count, one, total_n, s);
+    default:
+      return set_error(SELAS_EUNSUPPORTED, "int8_row_linear: streaming skinny kernel takes K = 1024, 2048, 3072");
   }
 }
 
@@ -1365,6 +1597,10 @@ extern "C" int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_
   const uint16_t *xb = static_cast<const uint16_t *>(x);
   const uint16_t *bb = static_cast<const uint16_t *>(bias);
   uint16_t *yb = static_cast<uint16_t *>(y);
+  if (M <= 32 && stream_k(K)) {
+    const GemvDesc one{qb, scale, bb, yb, N, ldy};
+    return launch_i8_gemv_stream(xb, ldx, M, K, nullptr, 1, one, N, s);
+  }
   if (M <= 32) {
     const int64_t grid = cdiv(N, 32 * kI8G);
     int8_row_gemv_kernel<<<dim3(static_cast<uint32_t>(grid)), dim3(kI8GemvThreads), 0, s>>>(
@@ -1405,4 +1641,28 @@ extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int
   return launch_gemv_stream(static_cast<const uint16_t *>(x), ldx, M, K,
                                 reinterpret_cast<const GemvDesc *>(descs), static_cast<int>(count), none,
                                 total_n, c, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int selas_int8_row_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx,
+                                             const selas_nf4_gemv_desc *descs, int64_t count, int64_t total_n,
+                                             int dtype, void *stream) {
+  if (M < 0 || K <= 0 || count < 0 || total_n < 0)
+    return set_error(SELAS_EINVAL, "int8_row_linear_grouped: bad shape M=%lld K=%lld count=%lld", (long long)M,
+                     (long long)K, (long long)count);
+  if (M == 0 || count == 0) return ok();
+  if (!x || !descs) return set_error(SELAS_EINVAL, "int8_row_linear_grouped: null pointer");
+  if (ldx < K) return set_error(SELAS_EINVAL, "int8_row_linear_grouped: ldx below K");
+  if (dtype != SELAS_BF16) return set_error(SELAS_EUNSUPPORTED, "int8_row_linear_grouped: takes bf16");
+  if (!stream_k(K) || M > 32 || count > kSgMaxDescs)
+    return set_error(SELAS_EUNSUPPORTED, "int8_row_linear_grouped: needs K = 1024, 2048 or 3072, M <= 32, "
+                                         "at most %d weights", kSgMaxDescs);
+  if (!aligned(x, 16) || ldx % 8 || !aligned(descs, 8))
+    return set_error(SELAS_EUNSUPPORTED, "int8_row_linear_grouped: x rows must be 16-byte aligned");
+  if (total_n <= 0 || total_n >= (1ll << 36))
+    return set_error(SELAS_EINVAL, "int8_row_linear_grouped: total_n must be the sum of the weights' row counts");
+  if (total_n * K >= (1ll << 32))
+    return set_error(SELAS_EUNSUPPORTED, "int8_row_linear_grouped: a weight above 4 GiB");
+  const GemvDesc none{nullptr, nullptr, nullptr, nullptr, 0, 0};
+  return launch_i8_gemv_stream(static_cast<const uint16_t *>(x), ldx, M, K, reinterpret_cast<const GemvDesc *>(descs),
+                               static_cast<int>(count), none, total_n, static_cast<hipStream_t>(stream));
 }

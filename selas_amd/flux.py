@@ -22,7 +22,7 @@ import torch.nn.functional as F
 
 from .codecs import EncodedTensor, encode_int8_row, encode_nf4, encode_raw
 from .kernels import FUSED, Kernels
-from .linear import UnitView, nf4_linear_grouped
+from .linear import UnitView, int8_row_linear_grouped, nf4_linear_grouped
 
 
 @dataclass
@@ -298,13 +298,20 @@ class RandomFlux:
 
         ``grouped`` runs all modulation linears in one launch (same bits as one call per linear)."""
         pre = self.mod_prefixes()
-        if grouped and all(u.tensors[p + ".weight"].codec == "nf4" for u, p in pre):
+        codecs = {u.tensors[p + ".weight"].codec for u, p in pre}
+        if grouped and codecs == {"nf4"}:
             ws = []
             for u, p in pre:
                 e = u.tensors[p + ".weight"]
                 ws.append((e.parts["packed"], e.parts["absmax"], int(e.meta["blocksize"]), e.meta["code"], e.shape,
                            u.get(p + ".bias")))
             ys = nf4_linear_grouped(sv, ws)
+        elif grouped and codecs == {"int8_row"}:
+            ws = []
+            for u, p in pre:
+                e = u.tensors[p + ".weight"]
+                ws.append((e.parts["q"], e.parts["scale"], e.shape, u.get(p + ".bias")))
+            ys = int8_row_linear_grouped(sv, ws)
         else:
             ys = [u.linear(sv, p) for u, p in pre]
         out, i = [], 0

@@ -261,16 +261,19 @@ def _gelu_chunk(codec: str, problems):
 
 
 class GroupedPlan:
-    """A prepared grouped skinny launch: fixed NF4 weights, any x with ``rows`` rows.
+    """A prepared grouped skinny launch: fixed NF4 (or int8_row) weights, any x with ``rows`` rows.
 
     ``weights``: sequence of (packed, absmax, blocksize, code, shape, bias) tuples sharing
-    K. The device descriptor table and the outputs are built once; ``run(x)`` is one
-    kernel launch and returns the plan's own output tensors, which the next ``run``
-    overwrites. ``supported`` is False when the grouped kernel does not cover the shapes
-    (then ``nf4_linear_grouped`` runs the linears one by one).
+    K; for ``codec="int8_row"`` (q, scale, None, None, shape, bias). The device descriptor
+    table and the outputs are built once; ``run(x)`` is one kernel launch and returns the
+    plan's own output tensors, which the next ``run`` overwrites. ``supported`` is False
+    when the grouped kernel does not cover the shapes (then ``nf4_linear_grouped`` runs the
+    linears one by one).
     """
 
-    def __init__(self, weights, rows: int, device: torch.device, dtype: torch.dtype = torch.bfloat16):
+    def __init__(self, weights, rows: int, device: torch.device, dtype: torch.dtype = torch.bfloat16,
+                 codec: str = "nf4"):
+        self.codec = codec
         self.weights = list(weights)
         self.rows = int(rows)
         self.k = int(self.weights[0][4][1]) if self.weights else 0
@@ -293,13 +296,16 @@ class GroupedPlan:
             total_n += n
         self.total_n = total_n
         self.desc = torch.tensor(rows_tbl, dtype=torch.int64).to(device)
-        self.code = _lib.code_array(self.weights[0][3])
+        self.code = _lib.code_array(self.weights[0][3]) if codec == "nf4" else None
 
     def _eligible(self, dtype) -> bool:
-        codes = {tuple(float(c) for c in w[3]) for w in self.weights}
+        if self.codec == "nf4":
+            codes = {tuple(float(c) for c in w[3]) for w in self.weights}
+            if len(codes) != 1 or any(int(w[2]) != 64 for w in self.weights):
+                return False
         return (dtype == torch.bfloat16 and 1 <= self.rows <= GROUPED_MAX_M and self.k in GROUPED_K
-                and len(codes) == 1 and len(self.weights) <= GROUPED_MAX_WEIGHTS
-                and all(int(w[2]) == 64 and len(w[4]) == 2 and int(w[4][1]) == self.k
+                and len(self.weights) <= GROUPED_MAX_WEIGHTS
+                and all(len(w[4]) == 2 and int(w[4][1]) == self.k
                         and w[0].data_ptr() % 16 == 0 and w[1].data_ptr() % 4 == 0 for w in self.weights))
 
     def run(self, x: torch.Tensor) -> list[torch.Tensor]:
@@ -311,8 +317,13 @@ class GroupedPlan:
             raise ValueError("x rows must be 16-byte aligned")
         dev = _lib.require_gpu(x2, self.desc)
         with torch.cuda.device(dev):
-            _lib.call("selas_nf4_linear_grouped", x2.data_ptr(), self.rows, self.k, x2.stride(0), self.desc.data_ptr(),
-                      len(self.weights), self.total_n, 64, self.code, _lib.BF16, _lib.stream(dev))
+            if self.codec == "nf4":
+                _lib.call("selas_nf4_linear_grouped", x2.data_ptr(), self.rows, self.k, x2.stride(0),
+                          self.desc.data_ptr(), len(self.weights), self.total_n, 64, self.code, _lib.BF16,
+                          _lib.stream(dev))
+            else:
+                _lib.call("selas_int8_row_linear_grouped", x2.data_ptr(), self.rows, self.k, x2.stride(0),
+                          self.desc.data_ptr(), len(self.weights), self.total_n, _lib.BF16, _lib.stream(dev))
         return self.outs
 
 
@@ -325,14 +336,22 @@ def nf4_linear_grouped(x: torch.Tensor, weights) -> list[torch.Tensor]:
     (selas/models/flux.py:428-445): every modulation linear of a model applied to one
     silu(vec). Shapes the grouped kernel does not cover are run one by one.
     """
-    weights = list(weights)
+    return _grouped("nf4", x, list(weights))
+
+
+def int8_row_linear_grouped(x: torch.Tensor, weights) -> list[torch.Tensor]:
+    """``nf4_linear_grouped`` for int8_row weights: (q, scale, shape, bias) tuples sharing ``x``."""
+    return _grouped("int8_row", x, [(q, s, None, None, shape, b) for q, s, shape, b in weights])
+
+
+def _grouped(codec: str, x: torch.Tensor, weights) -> list[torch.Tensor]:
     if not weights:
         return []
     dev = _lib.require_gpu(x, *(w[0] for w in weights))
     x2 = _rows(x)
-    plan = GroupedPlan(weights, x2.shape[0], dev, x.dtype)
+    plan = GroupedPlan(weights, x2.shape[0], dev, x.dtype, codec)
     if not plan.supported or x2.data_ptr() % 16 or x2.stride(0) % 8 or x2.shape[1] != plan.k:
-        return [nf4_linear(x, *w) for w in weights]
+        return [_single(codec, (x, *w)) for w in weights]
     outs = plan.run(x2)
     # The plan's descriptor table may be freed now: the caching allocator hands its memory
     # only to later work on this same stream, which runs after the launch.

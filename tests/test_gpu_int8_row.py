@@ -16,7 +16,7 @@ import torch
 from oracle import int8_row as oi8
 from oracle import nf4 as onf4
 from selas_amd import _lib, codecs
-from selas_amd.linear import (UnitView, int8_row_linear, int8_row_linear_batched, int8_row_linear_gelu)
+from selas_amd.linear import UnitView, int8_row_linear, int8_row_linear_batched, int8_row_linear_gelu
 
 from .conftest import seeded
 
@@ -194,3 +194,32 @@ def test_unit_view_dispatches_int8_row(dev):
         check_close(y.reshape(-1, n), oracle_linear(x.reshape(-1, k), w_ref, b.parts["data"]))
         (y2,) = view.linear_many([(x, "lin")])
         assert torch.equal(y, y2)
+
+
+def test_grouped_skinny_equals_one_by_one(dev):
+    from selas_amd.linear import int8_row_linear_grouped
+
+    shapes = [(3072 * 6, 3072), (192, 3072), (64, 3072), (100, 3072), (3072 * 3, 3072)]
+    ws, refs = [], []
+    for i, (n, k) in enumerate(shapes):
+        q, s, w_ref = make_weight(n, k, 40 + i, dev)
+        b = (torch.randn(n, generator=seeded(50 + i)) * 0.02).to(torch.bfloat16).to(dev) if i % 2 == 0 else None
+        ws.append((q, s, (n, k), b))
+        refs.append(w_ref)
+    for m in (1, 28, 32):
+        x = torch.nn.functional.silu(torch.randn(m, 1, 3072, generator=seeded(m))).to(torch.bfloat16).to(dev)
+        ys = int8_row_linear_grouped(x, ws)
+        for w, w_ref, y in zip(ws, refs, ys):
+            alone = int8_row_linear(x, *w)
+            assert y.shape == alone.shape == (m, 1, w[2][0])
+            assert torch.equal(y, alone)  # same bits as the per-linear call
+            check_close(y.reshape(m, -1), oracle_linear(x.reshape(m, -1), w_ref, w[3]))
+
+
+@pytest.mark.parametrize("k", [1024, 2048])
+def test_streaming_skinny_other_k(dev, k):
+    n, m = 416, 20
+    q, s, w_ref = make_weight(n, k, k, dev)
+    x = torch.randn(m, k, generator=seeded(k + 1)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(k + 2)) * 0.02).to(torch.bfloat16).to(dev)
+    check_close(int8_row_linear(x, q, s, (n, k), b), oracle_linear(x, w_ref, b))

@@ -182,13 +182,13 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(
 // bf16 (integers up to 256 are), and sum_k x u - 128 sum_k x = sum_k x q, the
 // second sum coming from one more MFMA against ones.
 //
+// This kernel serves K other than 1024, 2048, 3072 (those take int8_gemv_stream).
 // Workgroup: 32 output columns, all M rows; the eight waves take the K blocks
 // round-robin, three blocks in flight each, and their partial results are
-// summed in LDS in wave order (deterministic). Measured at M = 28, K = 3072:
-// 31 us for N = 18432 (1.8 TB/s of weights). Every variant tried (32 or 64
-// columns per workgroup, 2 to 6 blocks in flight, 2 or 4 waves per SIMD)
-// lands at 31-38 us: each 16-byte load touches 32 rows, 32 bytes of a 128-byte
-// line each, and the loads, not the waves in flight, set the rate.
+// summed in LDS in wave order (deterministic). Its 16-byte loads each touch 32
+// rows, 32 bytes of a 128-byte line per row, which holds it near 1.8 TB/s
+// (31 us for an 18432 x 3072 weight at M = 28) whatever the number of columns
+// per workgroup, loads in flight or waves per SIMD.
 constexpr int kI8GemvWaves = 8;
 constexpr int kI8GemvThreads = 64 * kI8GemvWaves;
 constexpr int kI8G = 1;  // 32-column groups per workgroup
@@ -1096,8 +1096,7 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   constexpr int LOOK = STAGES - 1;
   constexpr int XL = 4 * MB / NW;   // x DMAs (8 rows each) per K block and wave
   constexpr int LPB = 2 * CB + XL;  // vector-memory loads issued per K block and wave
-  static_assert(MB * CB * NW == 64 && (STAGES == 2 || STAGES == 3), "tile shape");
-  static_assert(XL % 2 == 0, "each wave's x rows start at a multiple of 16 (swizzle phase)");
+  static_assert(MB * CB * NW <= 64 && 4 * MB % NW == 0 && (STAGES == 2 || STAGES == 3), "tile shape");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB];
   const int t = (blockIdx.x & 7) * batch.per_xcd + (blockIdx.x >> 3);
   if (t >= batch.tiles) return;
@@ -1134,13 +1133,13 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // 16-byte chunk i%8, and so fetches logical chunk (i%8) ^ ((r/2)%8). With
   // that swizzle the 16 lanes one LDS cycle serves in a fragment read (16
   // consecutive rows, one logical chunk) hit 16 distinct 4-bank groups of the
-  // 64 banks. With XL even, (r/2)%8 = (4j + i/16) % 8 depends on j only
-  // through its parity.
+  // 64 banks. (r/2)%8 = (4(XL*w + j) + i/16) % 8 depends on w and j only
+  // through the parity of XL*w + j.
   uint32_t a_voff[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par)
     a_voff[par] = static_cast<uint32_t>(m0 + 8 * XL * wave + (lane >> 3)) * ldx_b +
-                  (static_cast<uint32_t>((lane & 7) ^ ((4 * par + (lane >> 4)) & 7)) << 4);
+                  (static_cast<uint32_t>((lane & 7) ^ ((4 * (par ^ ((XL * wave) & 1)) + (lane >> 4)) & 7)) << 4);
   const uint32_t a_vstep = 8u * ldx_b;
   uint8_t *const a_dst = smem + wave * XL * 1024;
   // Weight rows of this wave: n0 + WN*wave + 32*cb + c.
@@ -1359,7 +1358,7 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
     // stages HR*32 rows x WN columns at a time (row stride WN*2+8 bytes: the
     // 8-byte writes of 32 lanes then hit distinct banks), in its own region.
     constexpr int RS = WN * 2 + 8;
-    constexpr int HR = (NW * (MB / 2) * 32 * RS <= STAGES * SB) ? MB / 2 : 1;
+    constexpr int HR = (MB % 2 == 0 && NW * (MB / 2) * 32 * RS <= STAGES * SB) ? MB / 2 : 1;
     static_assert(NW * HR * 32 * RS <= STAGES * SB && MB % HR == 0, "epilogue staging fits the x stages");
     uint8_t *ep = smem + wave * HR * 32 * RS;
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(Yo, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldo * 2,
@@ -1446,11 +1445,21 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
   else nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
 }
 
-// Every launch uses 256 x 256 tiles of 4 waves (256 x 64 each), 3 LDS stages.
+// Tiles of 4 waves side by side (each 64 columns), 3 LDS stages, 256 rows
+// (MB = 8) or 224 rows (MB = 7), whichever finishes the launch in fewer
+// tile-rows of work: the tiles run in rounds of one per CU, so a launch of 216
+// 256-row tiles (M = 4608, N = 3072) leaves 40 CUs idle for its one round, while
+// its 252 224-row tiles do 7/8 of the work per CU in the same single round.
 // 128 x 512 tiles of 8 waves (128 x 64 each, two waves per SIMD) measured 15-25 %
 // slower: each decoded weight fragment then serves 4 MFMAs instead of 8.
 void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4) {
-  launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
+  auto rounds = [&](int tm) {
+    int64_t tiles = 0;
+    for (int i = 0; i < batch.count; ++i) tiles += cdiv(batch.p[i].M, tm) * cdiv(batch.p[i].N, 256);
+    return cdiv(tiles, cu_count());
+  };
+  if (rounds(224) * 7 < rounds(256) * 8) launch_gemm<7, 2, 3, 4>(batch, c, s, wc);
+  else launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
 }
 
 }  // namespace

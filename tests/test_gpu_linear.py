@@ -226,3 +226,19 @@ def test_gelu_epilogue_equals_linear_then_gelu(dev, m, n, k, gc, with_bias):
     assert (y is None) == (gc == n) and (y is None or torch.equal(y, full[:, :n - gc]))
     assert torch.count_nonzero(wide[:, :32]) == 0 and torch.count_nonzero(wide[:, 32 + gc:]) == 0
     check_close(full, oracle_linear(x, w_ref, b))
+
+
+def test_tile_height_does_not_change_the_bits(dev):
+    # M = 2048, N = 8192 runs 256-row tiles (256 tiles, one round); its first 300 rows alone run
+    # 224-row tiles (one round either way, fewer rows per tile). Every output sums K in the same
+    # order, so the bits agree; both are checked against the oracle.
+    n, k = 8192, 256
+    p, a, w_ref = make_weight(n, k, 61, dev)
+    x = torch.randn(2048, k, generator=seeded(62)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(63)) * 0.02).to(torch.bfloat16).to(dev)
+    big = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    small = nf4_linear(x[:300], p, a, 64, codecs.NF4_CODE, (n, k), b)
+    assert torch.equal(big[:300], small)
+    rows = torch.randint(0, 2048, (128,), generator=seeded(64))
+    check_close(big[rows], oracle_linear(x[rows], w_ref, b))
+    check_close(small, oracle_linear(x[:300], w_ref, b))

@@ -1113,7 +1113,8 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   const int64_t ldx = P.ldx, ldy = P.ldy;
   const int M = P.M, K = P.K, N = P.N, tiles_n = P.tiles_n;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // The wave index as a scalar: the LDS addresses of the x DMA (taken from M0) are then scalar arithmetic.
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, c = lane & 31;
   const int tm = (t - P.tile0) / tiles_n, tn = (t - P.tile0) - tm * tiles_n;
   const int m0 = tm * TM, n0 = tn * TN;

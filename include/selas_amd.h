@@ -284,19 +284,21 @@ int selas_attn_mlp(const void *attn, int64_t rows, int64_t Da, int64_t lda, cons
 /*
  * out[b, l, h*Dh + d] = sum_j softmax_j(q[b,h,l,:] . k[b,h,j,:] / sqrt(Dh)) v[b,h,j,d]
  * with q, k [B, H, L, Dh] contiguous, the values given transposed as vt
- * [B, H, Dh, L] (selas_transpose_heads), out [B, L, H*Dh] with row stride ldo
+ * [B, H, Dh, Lp] (selas_transpose_heads; Lp = L rounded up to a multiple of 64,
+ * the columns past L zero), out [B, L, H*Dh] with row stride ldo
  * (>= H*Dh; e.g. the first columns of the [attention | GELU(mlp)] input of the
  * single block's second linear, flux.py:198-200). bf16 in
  * and out; scores, softmax and sums in fp32, the probabilities rounded to bf16
  * for the second product (as the flash backends of torch's SDPA do). Takes
- * Dh = 128 and L % 128 == 0; otherwise SELAS_EUNSUPPORTED (the caller runs SDPA).
+ * Dh = 128 and any L; otherwise SELAS_EUNSUPPORTED (the caller runs SDPA).
  * Replaces _attention (flux.py:135-138).
  */
 int selas_attention(const void *q, const void *k, const void *vt, int64_t B, int64_t H, int64_t L, int64_t Dh,
                     void *out, int64_t ldo, int dtype, void *stream);
 
 /*
- * vt[i, d, l] = v[i, l, d] for BH heads of [L, Dh] (bf16, Dh = 128, L % 128 == 0):
+ * vt[i, d, l] = v[i, l, d] for BH heads of [L, Dh] (bf16, Dh = 128), with vt rows
+ * of Lp = L rounded up to a multiple of 64 tokens and vt[i, d, l] = 0 for l >= L:
  * the value layout selas_attention reads. No counterpart in the reference.
  */
 int selas_transpose_heads(const void *v, int64_t BH, int64_t L, int64_t Dh, void *vt, int dtype, void *stream);

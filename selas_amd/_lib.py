@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libselas_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2

@@ -4,9 +4,10 @@ The reference calls ``F.scaled_dot_product_attention(q, k, v)`` on q, k, v
 [B, H, L, Dh] and returns ``out.transpose(1, 2).reshape(B, L, H * Dh)``.
 ``attention`` computes the same with one fused kernel that writes the
 [B, L, H * Dh] layout directly (the transpose copy disappears). The values are
-read transposed ([B, H, Dh, L]), produced by ``transpose_heads``. Shapes outside
-the kernel (head dim other than 128, L not a multiple of 128, dtypes other than
-bf16) raise ``Unsupported``; ``flux.attention`` then runs SDPA, as the reference.
+read transposed ([B, H, Dh, L] padded to a multiple of 64 tokens), produced by
+``transpose_heads``. Any sequence length runs; shapes outside the kernel (head
+dim other than 128, dtypes other than bf16) raise ``Unsupported``;
+``flux.attention`` then runs SDPA, as the reference.
 """
 
 from __future__ import annotations
@@ -23,13 +24,14 @@ def _heads(t: torch.Tensor, what: str) -> torch.Tensor:
 
 
 def transpose_heads(v: torch.Tensor) -> torch.Tensor:
-    """v [B, H, L, Dh] -> [B, H, Dh, L] (contiguous)."""
+    """v [B, H, L, Dh] -> [B, H, Dh, Lp] (contiguous), Lp = L rounded up to 64 tokens; the
+    columns past L are zero."""
     v = _heads(v, "transpose_heads")
     b, h, l, d = v.shape
     dev = _lib.require_gpu(v)
     if v.dtype not in _lib.DTYPE_CODES:
         raise _lib.Unsupported(f"transpose_heads: dtype {v.dtype}")
-    vt = torch.empty(b, h, d, l, dtype=v.dtype, device=dev)
+    vt = torch.empty(b, h, d, (l + 63) // 64 * 64, dtype=v.dtype, device=dev)
     with torch.cuda.device(dev):
         _lib.call("selas_transpose_heads", v.data_ptr(), b * h, l, d, vt.data_ptr(), _lib.dtype_code(v.dtype),
                   _lib.stream(dev))
@@ -49,9 +51,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
     dev = _lib.require_gpu(q, k, v)
     if q.dtype not in _lib.DTYPE_CODES:
         raise _lib.Unsupported(f"attention: dtype {q.dtype}")
-    if d != 128 or l % 128 or q.dtype != torch.bfloat16:
-        raise _lib.Unsupported(f"attention: fused kernel takes bf16, head_dim 128 and L % 128 == 0 "
-                               f"(got {q.dtype}, {d}, {l})")
+    if d != 128 or q.dtype != torch.bfloat16:
+        raise _lib.Unsupported(f"attention: fused kernel takes bf16 and head_dim 128 (got {q.dtype}, {d})")
     if out is None:
         out = torch.empty(b, l, h * d, dtype=q.dtype, device=dev)
     elif (out.shape != (b, l, h * d) or out.dtype != q.dtype or out.device != q.device or out.stride(-1) != 1

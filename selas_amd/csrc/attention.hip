@@ -2,7 +2,7 @@
 // softmax(q k^T / sqrt(128)) v for every (batch, head), written straight into the
 // [B, L, H * 128] layout the projection linear reads.
 //
-// One workgroup = NWV waves (8 when L % 256 == 0 and L >= 3072, else 4) = 32 * NWV queries of
+// One workgroup = NWV waves (8 when L >= 3072, else 4) = 32 * NWV queries of
 // one (batch, head); wave w owns queries 32w .. 32w+31. The keys stream through
 // LDS in tiles of 64 (K rows and the matching V^T columns, double-buffered,
 // loaded by buffer->LDS DMA, shared by all the workgroup's waves). Per tile:
@@ -19,6 +19,9 @@
 //     MFMA k-step, and the V^T operand reads 8 consecutive keys (16 bytes).
 // LDS tiles are XOR-swizzled in 16-byte chunks so that the fragment reads (16
 // lanes per LDS cycle) hit 16 distinct 4-bank groups.
+// Any sequence length: key and query rows past L read as zeros (buffer range),
+// the last key tile's missing keys get score -inf, and query rows past L are not
+// stored; v^T rows are padded with zeros to a multiple of 64 tokens.
 //
 // LDS bandwidth bounds this kernel: every MFMA reads a 1 KiB A fragment from LDS
 // (halving those reads ran 24 % faster). Two query blocks per wave would share
@@ -32,7 +35,6 @@ namespace selas {
 namespace {
 
 constexpr int kDh = 128;                   // head dim
-constexpr int kQTMin = 128;                // queries per workgroup with 4 waves (the L granularity)
 constexpr int kKT = 64;                    // keys per tile
 constexpr int kTileBytes = kKT * kDh * 2;  // one K tile or V^T tile: 16 KiB
 constexpr int kStageBytes = 2 * kTileBytes;
@@ -69,11 +71,15 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c = lane & 31;
+  // q, k: [B*H, L, 128]; v^T: [B*H, 128, Lp] with Lp = L rounded up to the 64-key tile
+  // (zero-filled). Query and key rows past L read as zeros through the buffer range.
+  const int Lp = (L + kKT - 1) / kKT * kKT;
   const int64_t head = static_cast<int64_t>(bh) * L * kDh;  // elements
   const uint32_t head_bytes = static_cast<uint32_t>(L) * kDh * 2;
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q + head, head_bytes);
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(k + head, head_bytes);
-  const __amdgpu_buffer_rsrc_t vr = make_rsrc(vt + head, head_bytes);
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc(vt + static_cast<int64_t>(bh) * Lp * kDh,
+                                              static_cast<uint32_t>(Lp) * kDh * 2);
 
   // Q as the B operand of S^T = K Q^T: lane (query c of this wave, h) holds d = 16s + 8h .. +8.
   const int q_row = qt * kQT + 32 * wave + c;
@@ -94,7 +100,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
     const int r = 4 * J + (lane >> 4);
     k_voff[j] = static_cast<uint32_t>(r) * 256u + ((static_cast<uint32_t>(lane & 15) ^ (r & 15)) << 4);
     const int d = 8 * J + (lane >> 3);
-    v_voff[j] = static_cast<uint32_t>(d) * static_cast<uint32_t>(L) * 2u +
+    v_voff[j] = static_cast<uint32_t>(d) * static_cast<uint32_t>(Lp) * 2u +
                 ((static_cast<uint32_t>(lane & 7) ^ ((d >> 1) & 7)) << 4);
   }
   auto issue = [&](int stage, int kt) {
@@ -124,7 +130,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
 #pragma unroll
   for (int db = 0; db < 4; ++db) o[db] = f32x16{};
   float m_run = -__builtin_inff(), l_run = 0.0f;
-  const int ntiles = L / kKT;
+  const int ntiles = Lp / kKT;
 
   issue(0, 0);
   wait_vmcnt<0>();
@@ -138,6 +144,15 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
       sc[kb] = f32x16{};
 #pragma unroll
       for (int s = 0; s < 8; ++s) sc[kb] = mfma32(kfrag(stage, kb, s), qf[s], sc[kb]);
+    }
+    if (kt * kKT + kKT > L) {
+      // The last tile of a sequence that is not a multiple of 64: keys past L do not
+      // exist. Register r of score block kb holds key 32 kb + 16 (r/8) + 8 h + r % 8.
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kt * kKT + 32 * kb + 16 * (r >> 3) + 8 * h + (r & 7) >= L) sc[kb][r] = -__builtin_inff();
     }
     float mx = sc[0][0];
 #pragma unroll
@@ -190,6 +205,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
   // out[(b*L + q) * ldo + hh*128 + d] = O^T[d][q] / l, d = 32db + 8g + 4h + e for register 4g + e.
   const float inv = 1.0f / pair_sum(l_run);
   const int b = bh / H, hh = bh - b * H;
+  if (q_row >= L) return;  // a last query tile past the sequence end
   uint16_t *orow = out + (static_cast<int64_t>(b) * L + q_row) * ldo + hh * kDh;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -201,9 +217,10 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
     }
 }
 
-// vt[bh][d][l] = v[bh][l][d] for 64 tokens x 128 channels per workgroup, through LDS.
+// vt[bh][d][l] = v[bh][l][d] for 64 tokens x 128 channels per workgroup, through LDS;
+// vt rows hold Lp = L rounded up to 64 tokens, the ones past L zero.
 __global__ __launch_bounds__(256) void transpose_heads_kernel(const uint16_t *__restrict__ v, uint16_t *__restrict__ vt,
-                                                              int L) {
+                                                              int L, int Lp) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[kDh][kKT + 8];  // row stride 144 B
   const int l0 = blockIdx.x * kKT;
   const int64_t head = static_cast<int64_t>(blockIdx.y) * L * kDh;
@@ -211,7 +228,8 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(const uint16_t *__
 #pragma unroll
   for (int i = 0; i < 4; ++i) {  // token r, channels 8c .. 8c+7
     const int r = (tid >> 4) + 16 * i, ch = tid & 15;
-    const uint4 x = *reinterpret_cast<const uint4 *>(v + head + static_cast<int64_t>(l0 + r) * kDh + 8 * ch);
+    const uint4 x = l0 + r < L ? *reinterpret_cast<const uint4 *>(v + head + static_cast<int64_t>(l0 + r) * kDh + 8 * ch)
+                               : make_uint4(0, 0, 0, 0);
     const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -223,7 +241,8 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(const uint16_t *__
 #pragma unroll
   for (int i = 0; i < 4; ++i) {  // channel d, tokens 8c .. 8c+7
     const int d = (tid >> 3) + 32 * i, ch = tid & 7;
-    *reinterpret_cast<uint4 *>(vt + head + static_cast<int64_t>(d) * L + l0 + 8 * ch) =
+    *reinterpret_cast<uint4 *>(vt + static_cast<int64_t>(blockIdx.y) * Lp * kDh + static_cast<int64_t>(d) * Lp + l0 +
+                               8 * ch) =
         *reinterpret_cast<const uint4 *>(&tile[d][8 * ch]);
   }
 }
@@ -239,10 +258,10 @@ int check_heads(const char *what, int64_t B, int64_t H, int64_t L, int64_t Dh, i
     return set_error(SELAS_EINVAL, "%s: bad shape B=%lld H=%lld L=%lld Dh=%lld", what, (long long)B, (long long)H,
                      (long long)L, (long long)Dh);
   if (!valid_dtype(dtype)) return set_error(SELAS_EINVAL, "%s: bad dtype %d", what, dtype);
-  if (dtype != SELAS_BF16 || Dh != kDh || L % kQTMin)
-    return set_error(SELAS_EUNSUPPORTED, "%s: fused attention takes bf16, head_dim 128 and L %% 128 == 0 "
-                                         "(got %s, %lld, %lld)", what, dtype_name(dtype), (long long)Dh, (long long)L);
-  if (L * Dh * 2 >= (1ll << 32) || B * H >= (1ll << 31) / 64)
+  if (dtype != SELAS_BF16 || Dh != kDh)
+    return set_error(SELAS_EUNSUPPORTED, "%s: fused attention takes bf16 and head_dim 128 (got %s, %lld)", what,
+                     dtype_name(dtype), (long long)Dh);
+  if ((L + kKT) * Dh * 2 >= (1ll << 32) || B * H >= (1ll << 31) / 64)
     return set_error(SELAS_EUNSUPPORTED, "%s: a head above 4 GiB", what);
   return SELAS_OK;
 }
@@ -258,7 +277,7 @@ extern "C" int selas_attention(const void *q, const void *k, const void *vt, int
     return set_error(SELAS_EUNSUPPORTED, "attention: q, k, v^T must be 16-byte aligned, out rows 8-byte aligned");
   const float c2 = 1.4426950408889634f / sqrtf(static_cast<float>(Dh));  // log2(e) / sqrt(Dh)
   auto launch = [&](auto kernel, int nwv) {
-    const int qtiles = static_cast<int>(L / (32 * nwv));
+    const int qtiles = static_cast<int>(cdiv(L, 32 * nwv));
     const int64_t total = B * H * qtiles;
     const int per_xcd = static_cast<int>(cdiv(total, 8));
     kernel<<<dim3(static_cast<uint32_t>(per_xcd * 8)), dim3(64 * nwv), 0, static_cast<hipStream_t>(stream)>>>(
@@ -269,7 +288,7 @@ extern "C" int selas_attention(const void *q, const void *k, const void *vt, int
   // Eight waves share each tile among more queries but run one workgroup per CU:
   // at L = 4608 (FLUX 1024^2) 282 us against 297 with four, at L = 1536 159 against
   // 151 (each workgroup's fixed costs weigh more over 24 key tiles than over 72).
-  if (L % 256 == 0 && L >= 3072) launch(attn_fwd_kernel<8>, 8);
+  if (L >= 3072) launch(attn_fwd_kernel<8>, 8);
   else launch(attn_fwd_kernel<4>, 4);
   return check_launch("attention");
 }
@@ -282,8 +301,10 @@ extern "C" int selas_transpose_heads(const void *v, int64_t BH, int64_t L, int64
   if (!aligned(v, 16) || !aligned(vt, 16))
     return set_error(SELAS_EUNSUPPORTED, "transpose_heads: v and v^T must be 16-byte aligned");
   if (BH > 65535) return set_error(SELAS_EUNSUPPORTED, "transpose_heads: more than 65535 heads");
-  transpose_heads_kernel<<<dim3(static_cast<uint32_t>(L / kKT), static_cast<uint32_t>(BH)), dim3(256), 0,
+  const int64_t Lp = cdiv(L, kKT) * kKT;
+  transpose_heads_kernel<<<dim3(static_cast<uint32_t>(Lp / kKT), static_cast<uint32_t>(BH)), dim3(256), 0,
                            static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t *>(v),
-                                                               static_cast<uint16_t *>(vt), static_cast<int>(L));
+                                                               static_cast<uint16_t *>(vt), static_cast<int>(L),
+                                                               static_cast<int>(Lp));
   return check_launch("transpose_heads");
 }

@@ -93,20 +93,41 @@ def test_attention_deterministic_and_matches_sdpa(dev):
     check_close(F.sdpa_attention(q, k, v), reference(q, k, v))  # the library path meets the same bound
 
 
-def test_transpose_heads_exact(dev):
-    v = torch.randn(3, 2, 256, 128, generator=seeded(12)).to(torch.bfloat16).to(dev)
-    assert torch.equal(transpose_heads(v), v.transpose(-1, -2).contiguous())
+@pytest.mark.parametrize("l", [256, 100, 1])
+def test_transpose_heads_exact(dev, l):
+    # [B, H, Dh, Lp], Lp = L rounded up to 64, the columns past L zero.
+    v = torch.randn(3, 2, l, 128, generator=seeded(12)).to(torch.bfloat16).to(dev)
+    vt = transpose_heads(v)
+    lp = (l + 63) // 64 * 64
+    assert vt.shape == (3, 2, 128, lp)
+    assert torch.equal(vt[..., :l], v.transpose(-1, -2)) and torch.count_nonzero(vt[..., l:]) == 0
+
+
+@pytest.mark.parametrize("b,h,l", [(1, 2, 1), (2, 2, 65), (1, 3, 100), (1, 2, 130), (2, 1, 1000), (1, 2, 3100)])
+def test_any_sequence_length(dev, b, h, l):
+    # L not a multiple of the 64-key tile or of the query tile (3100: eight waves per workgroup):
+    # the last key tile is masked, the last query tile stored in part. FLUX at other resolutions
+    # (e.g. 768 x 1360: 4080 image + 512 text tokens) has such lengths.
+    q, k, v = qkv(b, h, l, 40 + l)
+    y = attention(q, k, v)
+    assert y.shape == (b, l, h * 128)
+    check_close(y, reference(q, k, v))
+    wide = torch.full((b * l + 3, h * 128 + 8), 7.0, dtype=torch.bfloat16, device=dev)
+    out = wide[:b * l].view(b, l, h * 128 + 8)[..., :h * 128]
+    attention(q, k, v, out=out)
+    assert torch.equal(out, y)
+    assert (wide[b * l:] == 7.0).all() and (wide[:, h * 128:] == 7.0).all()  # nothing written past the output
 
 
 def test_unsupported_shapes_fall_back_to_sdpa(dev):
-    for (l, d) in ((100, 128), (256, 64)):
-        g = seeded(l + d)
-        q, k, v = (torch.randn(1, 2, l, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
-        with pytest.raises(_lib.Unsupported):
-            attention(q, k, v)
-        y = F.attention(q, k, v)
-        assert y.shape == (1, l, 2 * d)
-        check_close(y, reference(q, k, v))
+    l, d = 256, 64
+    g = seeded(l + d)
+    q, k, v = (torch.randn(1, 2, l, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    with pytest.raises(_lib.Unsupported):
+        attention(q, k, v)
+    y = F.attention(q, k, v)
+    assert y.shape == (1, l, 2 * d)
+    check_close(y, reference(q, k, v))
 
 
 def test_attention_into_strided_rows(dev):
@@ -121,8 +142,8 @@ def test_attention_into_strided_rows(dev):
 
 @pytest.mark.parametrize("b,h,l", [(2, 2, 3072), (1, 3, 3328)])
 def test_eight_wave_workgroups(dev, b, h, l):
-    # L % 256 == 0 and L >= 3072 run 256 queries per workgroup (8 waves); the result meets the same
-    # bound, and a strided destination gets the same bits.
+    # L >= 3072 runs 256 queries per workgroup (8 waves); the result meets the same bound, and a
+    # strided destination gets the same bits.
     q, k, v = qkv(b, h, l, l + h)
     y = attention(q, k, v)
     g = seeded(l)

@@ -181,3 +181,21 @@ def test_planner_measurements(dev):
     prof = P.measure_profile(dev)
     assert prof.measured == ("attn_flops", "dequant_bw", "matmul_flops")
     assert 2e14 < prof.matmul_flops < 2.5e15 and 2e14 < prof.attn_flops < 2.5e15 and 2e11 < prof.dequant_bw < 8e12
+
+
+def test_blocks_at_a_token_count_off_the_tiles(model):
+    # 60 text + 7 x 7 image tokens = 109: attention's last key and query tiles are partial.
+    img, txt, cos, sin = inputs(1, 60, 7)
+    dev = torch.device("cuda")
+    x = torch.cat((txt, img), dim=1)
+    mod = (torch.randn(1, 3 * CFG.hidden, generator=seeded(33)) * 0.3).to(torch.bfloat16)
+    gx = F.single_block(model.singles[1], x.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
+                        False)
+    rx = OF.single_block(oracle_unit(model.singles[1]), x, mod.float(), cos, sin, OCFG, torch.float32, False)
+    assert rel(gx - x.cuda(), rx - x) < 2e-2 and rel(gx, rx) < 4e-3
+    dmod = (torch.randn(1, 12 * CFG.hidden, generator=seeded(34)) * 0.3).to(torch.bfloat16)
+    gi, gt = F.double_block(model.doubles[1], img.to(dev), txt.to(dev), dmod.to(dev), cos.to(dev), sin.to(dev), CFG,
+                            torch.bfloat16, False)
+    ri, rt = OF.double_block(oracle_unit(model.doubles[1]), img, txt, dmod.float(), cos, sin, OCFG, torch.float32,
+                             False)
+    assert rel(gi - img.cuda(), ri - img) < 2e-2 and rel(gt - txt.cuda(), rt - txt) < 2e-2

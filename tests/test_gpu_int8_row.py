@@ -223,3 +223,18 @@ def test_streaming_skinny_other_k(dev, k):
     x = torch.randn(m, k, generator=seeded(k + 1)).to(torch.bfloat16).to(dev)
     b = (torch.randn(n, generator=seeded(k + 2)) * 0.02).to(torch.bfloat16).to(dev)
     check_close(int8_row_linear(x, q, s, (n, k), b), oracle_linear(x, w_ref, b))
+
+
+def test_full_size_single_linear(dev):
+    # The 1536-token linear (W 12288 x 3072 ~ N(0, 0.02) seed 0, X 1536 x 3072 seed 1) with int8_row
+    # weights: rows sampled against the oracle.
+    n, k, m = 12288, 3072, 1536
+    w = torch.randn(n, k, generator=seeded(0)) * 0.02
+    e = codecs.encode_int8_row("w", w.to(dev))
+    x = torch.randn(m, k, generator=seeded(1)).to(torch.bfloat16).to(dev)
+    y = int8_row_linear(x, e.parts["q"], e.parts["scale"], (n, k))
+    w_ref = torch.from_numpy(onf4.bf16_to_f32(oi8.decode(e.parts["q"].cpu().numpy(), e.parts["scale"].cpu().numpy(),
+                                                        oi8.BF16))).view(n, k)
+    rows = torch.randint(0, m, (64,), generator=seeded(2))
+    check_close(y[rows], oracle_linear(x[rows], w_ref))
+    assert torch.isfinite(y).all()

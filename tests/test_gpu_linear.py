@@ -242,3 +242,19 @@ def test_tile_height_does_not_change_the_bits(dev):
     rows = torch.randint(0, 2048, (128,), generator=seeded(64))
     check_close(big[rows], oracle_linear(x[rows], w_ref, b))
     check_close(small, oracle_linear(x[:300], w_ref, b))
+
+
+_RNG_SHAPES = [(int(m), int(n), int(k)) for m, n, k in zip(
+    torch.randint(33, 700, (10,), generator=seeded(2024)).tolist(),
+    (torch.randint(1, 21, (10,), generator=seeded(2025)) * 64).tolist(),
+    (torch.randint(1, 17, (10,), generator=seeded(2026)) * 64).tolist())]
+
+
+@pytest.mark.parametrize("m,n,k", _RNG_SHAPES)
+def test_seeded_random_shapes(dev, m, n, k):
+    # Shapes drawn once from a seeded generator (M 33-699, N and K multiples of 64): both tile
+    # heights, partial row and column tiles, bias on odd draws.
+    p, a, w_ref = make_weight(n, k, m * 7 + n, dev)
+    x = torch.randn(m, k, generator=seeded(m + k)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(n)) * 0.02).to(torch.bfloat16).to(dev) if m % 2 else None
+    check_close(nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b), oracle_linear(x, w_ref, b))

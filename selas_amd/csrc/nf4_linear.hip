@@ -1446,20 +1446,26 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
   else nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
 }
 
-// Tiles of 4 waves side by side (each 64 columns), 3 LDS stages, 256 rows
-// (MB = 8) or 224 rows (MB = 7), whichever finishes the launch in fewer
-// tile-rows of work: the tiles run in rounds of one per CU, so a launch of 216
-// 256-row tiles (M = 4608, N = 3072) leaves 40 CUs idle for its one round, while
-// its 252 224-row tiles do 7/8 of the work per CU in the same single round.
+// Tiles of 4 waves side by side (each 64 columns), 3 LDS stages, and 256, 224
+// or 192 rows (MB = 8, 7, 6). The tiles run in rounds of one per CU; a launch
+// takes the height with the least rounds x relative tile time, the tile times
+// measured on the 1536-token linear (M 1536, N 12288, K 3072: one 256-row tile
+// 83 us, 224 rows 72 us, 192 rows 66 us; 128 rows measured slower again). There
+// 192-row tiles fill two rounds (384 tiles) where 256-row ones leave the second
+// round an eighth full: 165 -> 131 us. A launch of 216 256-row tiles (M 4608,
+// N 3072) takes 252 224-row ones, the same single round.
 // 128 x 512 tiles of 8 waves (128 x 64 each, two waves per SIMD) measured 15-25 %
 // slower: each decoded weight fragment then serves 4 MFMAs instead of 8.
 void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4) {
-  auto rounds = [&](int tm) {
+  auto cost = [&](int mb, double tile_time) {
     int64_t tiles = 0;
-    for (int i = 0; i < batch.count; ++i) tiles += cdiv(batch.p[i].M, tm) * cdiv(batch.p[i].N, 256);
-    return cdiv(tiles, cu_count());
+    for (int i = 0; i < batch.count; ++i) tiles += cdiv(batch.p[i].M, 32 * mb) * cdiv(batch.p[i].N, 256);
+    return static_cast<double>(cdiv(tiles, cu_count())) * tile_time;
   };
-  if (rounds(224) * 7 < rounds(256) * 8) launch_gemm<7, 2, 3, 4>(batch, c, s, wc);
+  // Smaller tiles only when they win by more than 2 % (ties keep the taller tile).
+  const double c8 = cost(8, 1.0), c7 = cost(7, 0.87), c6 = cost(6, 0.80);
+  if (c6 < 0.98 * c7 && c6 < 0.98 * c8) launch_gemm<6, 2, 3, 4>(batch, c, s, wc);
+  else if (c7 < 0.98 * c8) launch_gemm<7, 2, 3, 4>(batch, c, s, wc);
   else launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
 }
 

@@ -29,6 +29,7 @@
 // ran 25 % slower, because a lone wave cannot overlap its softmax with MFMAs.
 // Eight waves per workgroup (one workgroup per CU) share each tile's DMA among
 // 256 queries instead of 128, which cuts the LDS traffic per query by a tenth.
+#include <type_traits>
 #include "common.h"
 
 namespace selas {
@@ -136,18 +137,36 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
   wait_vmcnt<0>();
   __syncthreads();
 
-  auto tile = [&](int stage, int kt) {
+  // kMasked: the last tile of a sequence that is not a multiple of 64. The mask
+  // is a separate instantiation so that full tiles carry no per-score selects
+  // (a runtime test on every tile was turned into 93 selects and compares).
+  auto tile = [&](int stage, int kt, auto masked) {
+    constexpr bool kMasked = decltype(masked)::value;
     if (kt + 1 < ntiles) issue(stage ^ 1, kt + 1);
-    f32x16 sc[2];
+    // Scores: 16 MFMAs over (key block kb, d-chunk s) = (i / 8, i % 8). The K
+    // fragments go through a ring of kKAhead registers, each read kKAhead MFMAs
+    // before its use, so that no MFMA waits on a read issued just before it.
+    constexpr int kKAhead = 4;
+    f32x16 sc[2] = {f32x16{}, f32x16{}};
+    bf16x8 kf[kKAhead];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sc[kb] = f32x16{};
+    for (int i = 0; i < kKAhead; ++i) kf[i] = kfrag(stage, i / 8, i % 8);
 #pragma unroll
-      for (int s = 0; s < 8; ++s) sc[kb] = mfma32(kfrag(stage, kb, s), qf[s], sc[kb]);
+    for (int i = 0; i < 16; ++i) {
+      sc[i / 8] = mfma32(kf[i % kKAhead], qf[i % 8], sc[i / 8]);
+      if (i + kKAhead < 16) kf[i % kKAhead] = kfrag(stage, (i + kKAhead) / 8, (i + kKAhead) % 8);
     }
-    if (kt * kKT + kKT > L) {
-      // The last tile of a sequence that is not a multiple of 64: keys past L do not
-      // exist. Register r of score block kb holds key 32 kb + 16 (r/8) + 8 h + r % 8.
+    // The same order for the scheduler, which otherwise issues the first key
+    // block's reads right before their MFMAs where registers are tight.
+    __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kKAhead < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (kMasked) {
+      // Keys past L do not exist. Register r of score block kb holds key
+      // 32 kb + 16 (r/8) + 8 h + r % 8.
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -160,13 +179,22 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
     mx = pair_max(mx) * c2;
-    if (mx > m_run + 8.0f) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mx);
+    const bool raise = mx > m_run + 8.0f;
+    // Skipped for the whole wave unless some query's maximum moved (rare after the
+    // first tiles); lanes whose maximum stays multiply by exactly 1.
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+      const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] *= alpha;
       l_run *= alpha;
-      m_run = mx;
+      m_run = raise ? mx : m_run;
     }
+    // V^T fragments of the second product (db, kb, t2) = (i / 4, (i / 2) % 2, i % 2),
+    // the first kVAhead read before the exponentials, the rest kVAhead MFMAs ahead.
+    constexpr int kVAhead = 8;
+    bf16x8 vf[kVAhead];
+#pragma unroll
+    for (int i = 0; i < kVAhead; ++i) vf[i] = vfrag(stage, i / 4, (i / 2) % 2, i % 2);
     float ls = 0.0f;
     bf16x8 pb[2][2];
 #pragma unroll
@@ -185,22 +213,29 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
       }
     l_run += ls;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) o[db] = mfma32(vfrag(stage, db, kb, t2), pb[kb][t2], o[db]);
+    for (int i = 0; i < 16; ++i) {
+      o[i / 4] = mfma32(vf[i % kVAhead], pb[(i / 2) % 2][i % 2], o[i / 4]);
+      const int j = i + kVAhead;
+      if (j < 16) vf[i % kVAhead] = vfrag(stage, j / 4, (j / 2) % 2, j % 2);
+    }
     // The next tile has landed for this wave; the barrier then covers every wave
     // and orders this tile's LDS reads before the DMA that reuses its stage.
     wait_vmcnt<0>();
     __syncthreads();
   };
+  const std::integral_constant<bool, false> full{};
+  const std::integral_constant<bool, true> last{};
+  const int nfull = L / kKT;  // tiles whose 64 keys all exist
   int kt = 0;
-  for (; kt + 2 <= ntiles; kt += 2) {
-    tile(0, kt);
-    tile(1, kt + 1);
+  for (; kt + 2 <= nfull; kt += 2) {
+    tile(0, kt, full);
+    tile(1, kt + 1, full);
   }
-  if (kt < ntiles) tile(0, kt);
+  if (kt < nfull) tile(0, kt++, full);
+  if (kt < ntiles) {  // a partial last tile, stage kt % 2
+    if (kt & 1) tile(1, kt, last);
+    else tile(0, kt, last);
+  }
 
   // out[(b*L + q) * ldo + hh*128 + d] = O^T[d][q] / l, d = 32db + 8g + 4h + e for register 4g + e.
   const float inv = 1.0f / pair_sum(l_run);

@@ -253,10 +253,14 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
 }
 
 // vt[bh][d][l] = v[bh][l][d] for 64 tokens x 128 channels per workgroup, through LDS;
-// vt rows hold Lp = L rounded up to 64 tokens, the ones past L zero.
+// vt rows hold Lp = L rounded up to 64 tokens, the ones past L zero. The tile is
+// [token][channel] with a 65-word row: the row writes (lane = token r % 4, channel
+// chunk) fall in 64 distinct banks, and the transposed 2-byte reads (lane = channel d,
+// token chunk) in 32 distinct words, two lanes per word.
 __global__ __launch_bounds__(256) void transpose_heads_kernel(const uint16_t *__restrict__ v, uint16_t *__restrict__ vt,
                                                               int L, int Lp) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[kDh][kKT + 8];  // row stride 144 B
+  constexpr int kRow = kDh + 2;  // 260-byte rows
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kKT * kRow];
   const int l0 = blockIdx.x * kKT;
   const int64_t head = static_cast<int64_t>(blockIdx.y) * L * kDh;
   const int tid = threadIdx.x;
@@ -265,20 +269,23 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(const uint16_t *__
     const int r = (tid >> 4) + 16 * i, ch = tid & 15;
     const uint4 x = l0 + r < L ? *reinterpret_cast<const uint4 *>(v + head + static_cast<int64_t>(l0 + r) * kDh + 8 * ch)
                                : make_uint4(0, 0, 0, 0);
-    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      tile[8 * ch + 2 * e][r] = static_cast<uint16_t>(w[e]);
-      tile[8 * ch + 2 * e + 1][r] = static_cast<uint16_t>(w[e] >> 16);
-    }
+    uint32_t *dst = reinterpret_cast<uint32_t *>(tile + r * kRow + 8 * ch);  // 4-byte aligned
+    dst[0] = x.x;
+    dst[1] = x.y;
+    dst[2] = x.z;
+    dst[3] = x.w;
   }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 4; ++i) {  // channel d, tokens 8c .. 8c+7
     const int d = (tid >> 3) + 32 * i, ch = tid & 7;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = static_cast<uint32_t>(tile[(8 * ch + 2 * e) * kRow + d]) |
+             (static_cast<uint32_t>(tile[(8 * ch + 2 * e + 1) * kRow + d]) << 16);
     *reinterpret_cast<uint4 *>(vt + static_cast<int64_t>(blockIdx.y) * Lp * kDh + static_cast<int64_t>(d) * Lp + l0 +
-                               8 * ch) =
-        *reinterpret_cast<const uint4 *>(&tile[d][8 * ch]);
+                               8 * ch) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 

@@ -55,6 +55,16 @@ __device__ __forceinline__ float pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Two probabilities to packed bf16 (round to nearest even), one v_cvt_pk_bf16_f32.
+// The caller materializes each probability once, where it is produced, and adds
+// the same registers into the row sum; materializing again inside the pack made
+// the compiler copy every value (32 moves per tile).
+__device__ __forceinline__ uint32_t pack_probs(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 template <int NWV>
 __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *__restrict__ q,
                                                                const uint16_t *__restrict__ k,
@@ -204,10 +214,10 @@ __global__ __launch_bounds__(64 * NWV, 2) void attn_fwd_kernel(const uint16_t *_
         uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * t2 + 2 * e], c2, -m_run));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * t2 + 2 * e + 1], c2, -m_run));
+          const float p0 = materialize(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * t2 + 2 * e], c2, -m_run)));
+          const float p1 = materialize(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * t2 + 2 * e + 1], c2, -m_run)));
           ls += p0 + p1;
-          w[e] = pack_bf16x2(p0, p1);
+          w[e] = pack_probs(p0, p1);
         }
         pb[kb][t2] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
       }

@@ -230,7 +230,7 @@ def test_gelu_epilogue_equals_linear_then_gelu(dev, m, n, k, gc, with_bias):
 
 def test_tile_height_does_not_change_the_bits(dev):
     # M = 2048, N = 8192 runs 256-row tiles (256 tiles, one round); its first 300 rows alone run
-    # 224-row tiles (one round either way, fewer rows per tile). Every output sums K in the same
+    # 192-row tiles (one round either way, fewer rows per tile). Every output sums K in the same
     # order, so the bits agree; both are checked against the oracle.
     n, k = 8192, 256
     p, a, w_ref = make_weight(n, k, 61, dev)
@@ -242,6 +242,20 @@ def test_tile_height_does_not_change_the_bits(dev):
     rows = torch.randint(0, 2048, (128,), generator=seeded(64))
     check_close(big[rows], oracle_linear(x[rows], w_ref, b))
     check_close(small, oracle_linear(x[:300], w_ref, b))
+
+
+def test_224_row_tiles_give_the_same_bits(dev):
+    # On a 256-CU GPU, M = 448, N = 44032 (172 column tiles) runs 224-row tiles: 344 tiles in two
+    # rounds, where 192-row tiles would need three; its 2048-row superset runs 256-row tiles. The
+    # shared rows must agree bit for bit whichever heights the launches pick.
+    n, k = 44032, 64
+    p, a, w_ref = make_weight(n, k, 65, dev)
+    x = torch.randn(2048, k, generator=seeded(66)).to(torch.bfloat16).to(dev)
+    big = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k))
+    small = nf4_linear(x[:448], p, a, 64, codecs.NF4_CODE, (n, k))
+    assert torch.equal(big[:448], small)
+    rows = torch.randint(0, 448, (64,), generator=seeded(67))
+    check_close(small[rows], oracle_linear(x[rows], w_ref, None))
 
 
 _RNG_SHAPES = [(int(m), int(n), int(k)) for m, n, k in zip(

@@ -1482,10 +1482,12 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
   // One round of 256-row tiles that keeps at least 3/4 of the CUs busy: the chip
   // is then power-bound, shorter tiles in one round finish no sooner, and the
   // taller tile does the same work with fewer tiles (4608 x 3072 x 15360: 374 us
-  // with 256-row tiles, 390 us with 224, 574 us with 192).
+  // with 256-row tiles, 390 us with 224, 574 us with 192). The int8 operand's
+  // kernel keeps the cost model (256-row tiles made that shape slower).
   int64_t t8 = 0;
   for (int i = 0; i < batch.count; ++i) t8 += cdiv(batch.p[i].M, 256) * cdiv(batch.p[i].N, 256);
-  if (t8 <= cu_count() && 4 * t8 >= 3 * static_cast<int64_t>(cu_count())) launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
+  if (wc == WCodec::kNF4 && t8 <= cu_count() && 4 * t8 >= 3 * static_cast<int64_t>(cu_count()))
+    launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
   else if (c6 < 0.98 * c7 && c6 < 0.98 * c8) launch_gemm<6, 2, 3, 4>(batch, c, s, wc);
   else if (c7 < 0.98 * c8) launch_gemm<7, 2, 3, 4>(batch, c, s, wc);
   else launch_gemm<8, 2, 3, 4>(batch, c, s, wc);

@@ -2,21 +2,30 @@
 
 Restates selas/models/flux.py: FluxConfig 44-73, _attention 135-138,
 mlp_embed 150-151, double_block 300-324, single_block 327-338,
-final_layer 341-343, unit_flops 349-360, FluxRunner.svec 411-425 and the
-body of FluxRunner.step 527-582 without the step cache, plus the Euler update
-of selas/pipeline.py:489. Blocks take any ``w`` with ``.get``/``.linear`` and
-any ``k`` with the seven segment methods, exactly as the reference's do.
+final_layer 341-343, unit_flops 349-360, FluxRunner.svec 411-425,
+FluxRunner.modulations 428-445, FluxRunner.prepare 448-465 and the body of
+FluxRunner.step 527-582 without the step cache, plus the Euler update and the
+finiteness check of selas/pipeline.py:489-494. Blocks take any ``w`` with
+``.get``/``.linear`` and any ``k`` with the seven segment methods, exactly as
+the reference's do.
 
 ``OracleUnit`` is the checker's weight view: NF4 tensors are decoded with the
 reference decode (oracle.nf4) to the exact operand the reference multiplies
-with, and linears run in fp32 on the CPU.
+with. Its linears take the operands in the compute dtype and accumulate in
+fp32 with one rounding of the output to the compute dtype, which is the
+arithmetic of the GPU BLAS call the reference makes (F.linear in bf16); in
+fp32 they are plain fp32 linears.
 
 Pinned by golden vectors written with the reference's own functions
-(tests/golden/make_golden.py; tests/test_oracle_flux.py).
+(tests/golden/make_golden.py; tests/test_oracle_flux.py): the blocks in fp32
+and in bf16, rope_tables, timestep_embedding, mlp_embed, svec, modulations,
+prepare, two steps with their Euler updates; unit_flops against the totals
+the reference publishes (docs/PLAN.md:51-52).
 """
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import numpy as np
@@ -68,8 +77,9 @@ class OracleUnit:
         out = {}
         for name, (codec, shape, meta, parts) in enc.items():
             if codec == "nf4":
-                vals = onf4.decode(np.asarray(parts["packed"]), np.asarray(parts["absmax"]), int(meta["blocksize"]),
-                                   meta["code"], onf4.F32)
+                dec = onf4.c_decode if onf4.c_lib() else onf4.decode
+                vals = dec(np.asarray(parts["packed"]), np.asarray(parts["absmax"]), int(meta["blocksize"]),
+                           meta["code"], onf4.F32)
                 w = torch.from_numpy(vals).view(*shape).to(operand_dtype).float()
             elif codec == "int8_row":
                 out_code = {torch.bfloat16: oi8.BF16, torch.float16: oi8.F16, torch.float32: oi8.F32}[operand_dtype]
@@ -91,16 +101,34 @@ class OracleUnit:
         return self.t[name].to(dtype or self.dtype)
 
     def linear(self, x, prefix, dtype=None):
+        """F.linear in the compute dtype: operands rounded to it, fp32 accumulation, bias added in fp32,
+        one rounding of the result (fp32 compute dtype: a plain fp32 linear)."""
         dt = dtype or self.dtype
-        w = self.t[prefix + ".weight"].to(dt)
+        w = self.t[prefix + ".weight"].to(dt).float()
         b = self.t.get(prefix + ".bias")
-        return F.linear(x.to(dt), w, None if b is None else b.to(dt))
+        y = F.linear(x.to(dt).float(), w, None if b is None else b.to(dt).float())
+        return y.to(dt)
 
 
 def attention(q, k, v):
-    """Scaled dot-product attention over [B, H, L, Dh] -> [B, L, H*Dh] (flux.py:135-138), in fp32."""
+    """Scaled dot-product attention over [B, H, L, Dh] -> [B, L, H*Dh] (flux.py:135-138).
+
+    fp32 inputs: fp32 SDPA. bf16 / fp16 inputs: the arithmetic of torch's flash backends, which the
+    reference's SDPA call runs on a GPU in those dtypes: fp32 scores and softmax, the probabilities
+    exp(s - rowmax) rounded to the compute dtype for the product with v, fp32 row sums of the
+    unrounded probabilities, fp32 accumulation and one rounding of the output. (A flash kernel
+    subtracts a running maximum tile by tile; with the final maximum the roundings differ only
+    where that maximum moved.)"""
     b, h, l, d = q.shape
-    out = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).to(q.dtype)
+    if q.dtype == torch.float32:
+        out = F.scaled_dot_product_attention(q, k.float(), v.float())
+    else:
+        out = torch.empty_like(q)
+        for i in range(b):  # one [L, L] score matrix at a time
+            for j in range(h):
+                s = (q[i, j].float() @ k[i, j].float().t()) / math.sqrt(d)
+                p = torch.exp(s - s.amax(-1, keepdim=True))
+                out[i, j] = ((p.to(q.dtype).float() @ v[i, j].float()) / p.sum(-1, keepdim=True)).to(q.dtype)
     return out.transpose(1, 2).reshape(b, l, h * d)
 
 
@@ -168,3 +196,67 @@ def svec(g, cfg: FluxConfig, sigmas, guidance: float, pooled: torch.Tensor, dt) 
         vec = vec + mlp_embed(g, "guidance_in", timestep_embedding(gv, 256).to(dt)).float()[None]
     vec = vec + mlp_embed(g, "vector_in", pooled.to(dt)).float()[None]
     return F.silu(vec).to(dt)
+
+
+def modulations(mod_units, svecs, n_double: int):
+    """Every block's modulation vectors [S, 1, kD] per image (flux.py:428-445): double blocks concatenate
+    the image and text linears, single blocks have one; ``mod_units`` in block order."""
+    outs = []
+    for sv in svecs:
+        per = []
+        for i, w in enumerate(mod_units):
+            if i < n_double:
+                per.append(torch.cat((w.linear(sv, "img_mod.lin"), w.linear(sv, "txt_mod.lin")), dim=-1))
+            else:
+                per.append(w.linear(sv, "modulation.lin"))
+        outs.append(per)
+    return outs
+
+
+@dataclass
+class Conditioning:
+    """FluxConditioning (flux.py:365-373) for the oracle."""
+
+    sigmas: list
+    mods: list  # per block [S, B, kD]
+    final_mod: torch.Tensor  # [S, B, 2D]
+    txt: torch.Tensor  # [B, Lt, D] fp32
+    cos: torch.Tensor
+    sin: torch.Tensor
+    l_txt: int
+
+
+def prepare(g, cfg: FluxConfig, sigmas, guidance: float, pooled, txt, img_ids, txt_ids, mods, dt) -> Conditioning:
+    """FluxRunner.prepare (flux.py:448-465) with the batch's modulations given ([S, B, kD] per block)."""
+    from .segments import rope_tables
+
+    svecs = [svec(g, cfg, sigmas, guidance, pooled[i:i + 1], dt) for i in range(pooled.shape[0])]
+    final_mod = torch.cat([g.linear(sv, "final_layer.adaLN_modulation.1") for sv in svecs], dim=1)
+    txt_h = g.linear(txt.to(dt), "txt_in").float()
+    ids = torch.cat((txt_ids, img_ids), dim=0)
+    cos, sin = rope_tables(ids, cfg.axes_dim, cfg.theta)
+    return Conditioning(list(sigmas), mods, final_mod, txt_h, cos, sin, txt.shape[1])
+
+
+def step(g, doubles, singles, cfg: FluxConfig, s: int, latents, cond: Conditioning, dt, k=OracleKernels,
+         attn=attention):
+    """Velocity for step ``s`` (FluxRunner.step, flux.py:527-582, without the step cache)."""
+    guard = dt == torch.float16
+    img = g.linear(latents.to(dt), "img_in").float()
+    txt = cond.txt
+    nd = len(doubles)
+    for i, w in enumerate(doubles):
+        img, txt = double_block(w, img, txt, cond.mods[i][s], cond.cos, cond.sin, cfg, dt, guard, k, attn)
+    x = torch.cat((txt, img), dim=1)
+    for j, w in enumerate(singles):
+        x = single_block(w, x, cond.mods[nd + j][s], cond.cos, cond.sin, cfg, dt, guard, k, attn)
+    return final_layer(g, x[:, cond.l_txt:], cond.final_mod[s], dt, k)
+
+
+def euler(x, sigmas, s: int, pred):
+    """One sampler update x + (sigma[s+1] - sigma[s]) * v, then the finiteness check that raises
+    FloatingPointError on non-finite latents (selas/pipeline.py:489-494)."""
+    x = x + (sigmas[s + 1] - sigmas[s]) * pred
+    if not bool(torch.isfinite(x).all()):
+        raise FloatingPointError(f"non-finite latents after step {s + 1}/{len(sigmas) - 1}")
+    return x

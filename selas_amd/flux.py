@@ -1,15 +1,18 @@
 """FLUX.1 blocks and step on the gfx950 kernels: the callers of the NF4 hot path.
 
 The block functions follow selas/models/flux.py (double_block 300-324,
-single_block 327-338, final_layer 341-343, FluxRunner.step 527-582 without the
-step cache, modulation hoisting 411-445) with ``w.linear`` going to the fused
+single_block 327-338, final_layer 341-343) with ``w.linear`` going to the fused
 NF4 linear and ``k`` defaulting to the fused segment kernels. Attention is the
-library SDPA call the reference makes (flux.py:135-138), restricted to the
-fused flash / memory-efficient backends.
+fused gfx950 kernel (selas_amd.attention) in place of the reference's SDPA call
+(flux.py:135-138), with SDPA for the shapes the kernel does not take.
 
 ``RandomFlux`` builds a FLUX-shaped model with random weights NF4-encoded on
 the GPU (the reference's convert step quantizes every 2-D block weight, keeps
 norm scales in fp32, biases and the ``globals`` unit raw: convert.py:144-187).
+``FluxRunner`` drives it as the reference's runner does: svec (flux.py:411-425),
+the hoisted modulations (428-445), prepare (448-465), step (527-582, without
+the step cache) and the sampler loop's Euler update with its finiteness check
+(selas/pipeline.py:483-494).
 """
 
 from __future__ import annotations
@@ -76,8 +79,8 @@ def sdpa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.T
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """[B, H, L, Dh] -> [B, L, H*Dh]: the fused gfx950 kernel (selas_amd.attention), or SDPA for the
-    shapes it does not take (head dim other than 128, L not a multiple of 128). ``out``: optional
+    """[B, H, L, Dh] -> [B, L, H*Dh]: the fused gfx950 kernel (selas_amd.attention, any L), or SDPA for
+    the shapes it does not take (head dim other than 128, dtypes other than bf16). ``out``: optional
     destination with equally spaced rows (returned)."""
     from . import _lib
     from .attention import attention as fused_attention
@@ -339,3 +342,156 @@ class RandomFlux:
         for j, w in enumerate(self.singles):
             x = single_block(w, x, mods_s[nd + j], cos, sin, cfg, dt, guard, k)
         return final_layer(self.globals, x[:, lt:], final_mod_s, dt, k)
+
+
+# --------------------------------------------------------------------------- runner
+
+
+def timestep_embedding(t: torch.Tensor, dim: int = 256, max_period: float = 10000.0,
+                       time_factor: float = 1000.0) -> torch.Tensor:
+    """Sinusoidal embedding [N, dim] fp32 of times t [N] on t's device (flux.py:95-103)."""
+    t = time_factor * t.float()
+    half = dim // 2
+    freqs = torch.exp(-math.log(max_period) * torch.arange(half, dtype=torch.float32, device=t.device) / half)
+    args = t[:, None] * freqs[None]
+    emb = torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+    if dim % 2:
+        emb = torch.cat([emb, torch.zeros_like(emb[:, :1])], dim=-1)
+    return emb
+
+
+def mlp_embed(w, prefix: str, x: torch.Tensor) -> torch.Tensor:
+    """in_layer, SiLU, out_layer (flux.py:150-151)."""
+    return w.linear(F.silu(w.linear(x, prefix + ".in_layer")), prefix + ".out_layer")
+
+
+def text_ids(length: int, device=None) -> torch.Tensor:
+    """Zero position ids [length, 3] of the text tokens (selas/sampling.py:68-69)."""
+    return torch.zeros(length, 3, device=device)
+
+
+def get_schedule(num_steps: int, image_seq_len: int, base_shift: float = 0.5, max_shift: float = 1.15,
+                 shift: bool = True) -> list[float]:
+    """num_steps + 1 sigmas from 1 to 0 with FLUX-dev's resolution-dependent shift (selas/sampling.py:10-27)."""
+    ts = [1.0 - i / num_steps for i in range(num_steps + 1)]
+    if not shift:
+        return ts
+    x1, x2 = 256.0, 4096.0
+    slope = (max_shift - base_shift) / (x2 - x1)
+    mu = slope * image_seq_len + (base_shift - slope * x1)
+
+    def shifted(t: float) -> float:
+        if t <= 0.0:
+            return 0.0
+        if t >= 1.0:
+            return 1.0
+        return math.exp(mu) / (math.exp(mu) + (1.0 / t - 1.0))
+
+    return [shifted(t) for t in ts]
+
+
+@dataclass
+class FluxConditioning:
+    """Everything a step needs besides the latents (flux.py:365-373): per block [S, B, kD] modulations,
+    the final layer's [S, B, 2D], the text stream after txt_in [B, Lt, D] fp32 and the RoPE tables."""
+
+    sigmas: list
+    mods: dict
+    final_mod: torch.Tensor
+    txt: torch.Tensor
+    cos: torch.Tensor
+    sin: torch.Tensor
+    l_txt: int
+
+
+@dataclass
+class StepInfo:
+    """What a step did (flux.py:376-379): every step here runs in full."""
+
+    decision: str = "full"
+    distance: float | None = None
+
+
+class FluxRunner:
+    """The reference runner's prologue and step (flux.py:392-582) over a model whose units are resident
+    on one GPU (``RandomFlux``): no weight streaming, every modulation linear of an image in one grouped
+    launch. Block names follow the reference ("double.i", "single.j")."""
+
+    def __init__(self, model: RandomFlux, kernels: Kernels = FUSED):
+        self.model = model
+        self.k = kernels
+        self.cfg = model.cfg
+        self.dt = model.dt
+        self.guard = model.dt == torch.float16
+        self.g = model.globals
+        self.doubles = [f"double.{i}" for i in range(len(model.doubles))]
+        self.singles = [f"single.{i}" for i in range(len(model.singles))]
+        self.main = self.doubles + self.singles
+
+    @torch.no_grad()
+    def svec(self, sigmas, guidance: float, pooled: torch.Tensor) -> torch.Tensor:
+        """silu(vec) [S, 1, D] for one image (``pooled`` [1, vec_dim]): timestep + guidance + pooled-text
+        embeddings (flux.py:411-425)."""
+        cfg, g, dt, dev = self.cfg, self.g, self.dt, self.model.device
+        t = torch.tensor(list(sigmas[:-1]), dtype=torch.float32, device=dev)
+        vec = mlp_embed(g, "time_in", timestep_embedding(t, 256).to(dt)).float()[:, None, :]
+        if cfg.guidance_embed:
+            gv = torch.full((1,), float(guidance), dtype=torch.float32, device=dev)
+            vec = vec + mlp_embed(g, "guidance_in", timestep_embedding(gv, 256).to(dt)).float()[None]
+        vec = vec + mlp_embed(g, "vector_in", pooled.to(dev, dt)).float()[None]
+        return F.silu(vec).to(dt)
+
+    @torch.no_grad()
+    def modulations(self, svecs: list[torch.Tensor]) -> list[dict[str, torch.Tensor]]:
+        """Every block's modulation vectors [S, 1, kD] for each image's svec (flux.py:428-445)."""
+        return [dict(zip(self.main, self.model.modulations(sv))) for sv in svecs]
+
+    @torch.no_grad()
+    def prepare(self, sigmas, guidance: float, pooled: torch.Tensor, txt: torch.Tensor, img_ids: torch.Tensor,
+                txt_ids: torch.Tensor, mods: dict[str, torch.Tensor] | None = None) -> FluxConditioning:
+        """Everything that does not depend on the latents, once per batch (flux.py:448-465). ``mods``: the
+        batch's modulation vectors {block: [S, B, kD]} when already known."""
+        cfg, g, dt, dev = self.cfg, self.g, self.dt, self.model.device
+        svecs = [self.svec(sigmas, guidance, pooled[i:i + 1]) for i in range(pooled.shape[0])]
+        if mods is None:
+            per_image = self.modulations(svecs)
+            mods = {n: torch.cat([m[n] for m in per_image], dim=1) for n in self.main}
+        final_mod = torch.cat([g.linear(sv, "final_layer.adaLN_modulation.1") for sv in svecs], dim=1)
+        txt_h = g.linear(txt.to(dev, dt), "txt_in").float()
+        ids = torch.cat((txt_ids, img_ids), dim=0).to(dev)
+        cos, sin = rope_tables(ids, cfg.axes_dim, cfg.theta)
+        return FluxConditioning(list(sigmas), mods, final_mod, txt_h, cos, sin, txt.shape[1])
+
+    @torch.no_grad()
+    def step(self, s: int, latents: torch.Tensor, cond: FluxConditioning, cache=None):
+        """Velocity for step ``s`` from packed latents [B, Li, 64] fp32 (flux.py:527-582): (velocity, StepInfo).
+        The reference's optional step cache is not part of this path: ``cache`` must be None or inactive."""
+        if cache is not None and getattr(cache, "active", False):
+            raise NotImplementedError("the step cache is not supported by selas_amd's runner")
+        mods_s = [cond.mods[n][s] for n in self.main]
+        out = self.model.step(latents, cond.txt, mods_s, cond.final_mod[s], cond.cos, cond.sin, self.k)
+        return out, StepInfo()
+
+    @torch.no_grad()
+    def denoise(self, x: torch.Tensor, cond: FluxConditioning, on_step=None) -> torch.Tensor:
+        """The sampler loop (selas/pipeline.py:483-494): per step the velocity, the Euler update
+        x + (sigma[s+1] - sigma[s]) * v and a check that the latents stay finite (FloatingPointError
+        otherwise). ``on_step(s, steps)`` is called after each step."""
+        sig = cond.sigmas
+        steps = len(sig) - 1
+        for s in range(steps):
+            pred, _ = self.step(s, x, cond)
+            x = euler_update(x, sig, s, pred, self.dt)
+            if on_step is not None:
+                on_step(s, steps)
+        return x
+
+
+def euler_update(x: torch.Tensor, sigmas, s: int, pred: torch.Tensor, dt=torch.bfloat16) -> torch.Tensor:
+    """x + (sigma[s+1] - sigma[s]) * pred, raising FloatingPointError when the result is not finite
+    (selas/pipeline.py:489-494)."""
+    x = x + (sigmas[s + 1] - sigmas[s]) * pred
+    if not bool(torch.isfinite(x).all()):
+        hint = " (fp16 overflow: retry with --dtype fp32)" if dt == torch.float16 else ""
+        raise FloatingPointError(f"non-finite latents after step {s + 1}/{len(sigmas) - 1} in {dt}{hint}")
+    return x

@@ -48,6 +48,18 @@ def _vec(v: torch.Tensor, b: int, d: int, what: str) -> tuple[torch.Tensor, int]
     return v, (sb if vb > 1 else 0)
 
 
+def _vec_pair(shift: torch.Tensor, scale: torch.Tensor, b: int, d: int, what: str):
+    """shift and scale with one shared batch stride: where one is per batch ([B, 1, D]) and the other
+    broadcast ([1, 1, D]), both are laid out per batch (a [B, D] copy of at most B*D floats)."""
+    shift, msb = _vec(shift, b, d, what + " shift")
+    scale, csb = _vec(scale, b, d, what + " scale")
+    if msb == csb:
+        return shift, scale, msb
+    shift = shift.reshape(-1, d).expand(b, d).contiguous()
+    scale = scale.reshape(-1, d).expand(b, d).contiguous()
+    return shift, scale, d
+
+
 def _f32_rows(x: torch.Tensor, what: str) -> torch.Tensor:
     if x.dtype != torch.float32:
         raise ValueError(f"{what}: the residual stream must be float32, got {x.dtype}")
@@ -65,10 +77,7 @@ class Kernels:
         x = _f32_rows(x, "mod_in")
         dev = _lib.require_gpu(x, shift, scale)
         b, l, d, sb, sl = _bld(x, "mod_in")
-        shift, msb = _vec(shift, b, d, "mod_in shift")
-        scale, csb = _vec(scale, b, d, "mod_in scale")
-        if msb != csb:
-            raise ValueError("mod_in: shift and scale must share a batch stride")
+        shift, scale, msb = _vec_pair(shift, scale, b, d, "mod_in")
         out = torch.empty(*x.shape, dtype=dt, device=dev)
         with torch.cuda.device(dev):
             _lib.call("selas_mod_in", x.data_ptr(), b, l, d, sb, sl, shift.data_ptr(), scale.data_ptr(), msb,
@@ -99,10 +108,7 @@ class Kernels:
                 _lib.call("selas_gated_add", x.data_ptr(), b, l, d, sb, sl, g.data_ptr(), gsb, y.data_ptr(),
                           _lib.dtype_code(y.dtype), ysb, ysl, int(bool(guard)), x_out.data_ptr(), _lib.stream(dev))
                 return x_out, None
-            shift, msb = _vec(shift, b, d, what + " shift")
-            scale, csb = _vec(scale, b, d, what + " scale")
-            if msb != csb:
-                raise ValueError(f"{what}: shift and scale must share a batch stride")
+            shift, scale, msb = _vec_pair(shift, scale, b, d, what)
             h = torch.empty(*x.shape, dtype=dt, device=dev)
             _lib.call("selas_gated_add_mod", x.data_ptr(), b, l, d, sb, sl, g.data_ptr(), gsb, y.data_ptr(),
                       _lib.dtype_code(y.dtype), ysb, ysl, int(bool(guard)), shift.data_ptr(), scale.data_ptr(), msb,

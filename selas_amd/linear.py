@@ -34,6 +34,31 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
     return x.reshape(-1, k).contiguous()
 
 
+def _check_nf4_parts(packed: torch.Tensor, absmax: torch.Tensor, numel: int, blocksize: int) -> None:
+    """The kernels read N*K/2 code bytes and N*K/blocksize fp32 scales from the parts' base pointers."""
+    if packed.dtype != torch.uint8 or not packed.is_contiguous() or packed.numel() * 2 != numel:
+        raise ValueError(f"packed NF4 data must be contiguous uint8 with {numel // 2} bytes, got {packed.dtype} "
+                         f"{tuple(packed.shape)}")
+    if blocksize <= 0 or numel % blocksize:
+        raise ValueError(f"nf4 needs numel divisible by blocksize ({numel} % {blocksize})")
+    if absmax.dtype != torch.float32 or not absmax.is_contiguous() or absmax.numel() != numel // blocksize:
+        raise ValueError(f"NF4 absmax must be contiguous float32 with {numel // blocksize} values, got "
+                         f"{absmax.dtype} {tuple(absmax.shape)}")
+
+
+def _check_int8_parts(q: torch.Tensor, scale: torch.Tensor, n: int, k: int) -> None:
+    if q.dtype != torch.int8 or not q.is_contiguous() or q.numel() != n * k:
+        raise ValueError(f"int8_row data must be contiguous int8 with {n * k} values, got {q.dtype} {tuple(q.shape)}")
+    if scale.dtype != torch.float32 or not scale.is_contiguous() or scale.numel() != n:
+        raise ValueError(f"int8_row scale must be contiguous float32 with {n} values, got {scale.dtype} "
+                         f"{tuple(scale.shape)}")
+
+
+def _check_bias(bias: torch.Tensor | None, n: int) -> None:
+    if bias is not None and bias.numel() != n:
+        raise ValueError(f"bias has {bias.numel()} values, the weight has {n} rows")
+
+
 def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, blocksize: int, code, shape,
                bias: torch.Tensor | None = None) -> torch.Tensor:
     """``F.linear(x, decode(W), bias)`` for an NF4 weight ``W`` of ``shape`` [N, K]."""
@@ -43,11 +68,13 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
     if x.shape[-1] != k:
         raise ValueError(f"x has {x.shape[-1]} features, weight expects {k}")
     dev = _lib.require_gpu(x, packed, absmax, bias)
+    _check_nf4_parts(packed, absmax, n * k, int(blocksize))
     x2 = _rows(x)
     m = x2.shape[0]
     y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
     if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
         bias = bias.to(x.dtype).contiguous()
+    _check_bias(bias, n)
     try:
         if x.dtype not in _lib.DTYPE_CODES:
             raise _lib.Unsupported(f"dtype {x.dtype}")
@@ -71,11 +98,13 @@ def int8_row_linear(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, shape
     if x.shape[-1] != k:
         raise ValueError(f"x has {x.shape[-1]} features, weight expects {k}")
     dev = _lib.require_gpu(x, q, scale, bias)
+    _check_int8_parts(q, scale, n, k)
     x2 = _rows(x)
     m = x2.shape[0]
     y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
     if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
         bias = bias.to(x.dtype).contiguous()
+    _check_bias(bias, n)
     try:
         if x.dtype not in _lib.DTYPE_CODES:
             raise _lib.Unsupported(f"dtype {x.dtype}")
@@ -150,6 +179,13 @@ def _batched(codec: str, problems):
     return outs
 
 
+def _check_parts(codec: str, a: torch.Tensor, b: torch.Tensor, n: int, k: int, blocksize) -> None:
+    if codec == "nf4":
+        _check_nf4_parts(a, b, n * k, int(blocksize))
+    else:
+        _check_int8_parts(a, b, n, k)
+
+
 def _batched_chunk(codec: str, problems):
     code = _batch_eligible(codec, problems)
     if code is False:
@@ -157,13 +193,15 @@ def _batched_chunk(codec: str, problems):
     dev = _lib.require_gpu(*(p[0] for p in problems), *(p[1] for p in problems))
     arr = (_lib.GemmProblem * len(problems))()
     outs, keep = [], []
-    for i, (x, packed, absmax, _, _, shape, bias) in enumerate(problems):
+    for i, (x, packed, absmax, bs, _, shape, bias) in enumerate(problems):
         n, k = int(shape[0]), int(shape[1])
         if len(shape) != 2 or x.shape[-1] != k:
             raise ValueError(f"x has {x.shape[-1]} features, weight {tuple(shape)} expects {k}")
+        _check_parts(codec, packed, absmax, n, k, bs)
         x2 = _rows(x)
         if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
             bias = bias.to(x.dtype).contiguous()
+        _check_bias(bias, n)
         y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
         keep += [x2, bias]
         outs.append(y)
@@ -223,15 +261,17 @@ def _gelu_chunk(codec: str, problems):
     dev = _lib.require_gpu(*(p[0] for p in problems), *(p[1] for p in problems))
     arr = (_lib.GemmProblem * len(problems))()
     outs, keep = [], []
-    for i, (x, packed, absmax, _, _, shape, bias, gelu_cols, gelu_out) in enumerate(problems):
+    for i, (x, packed, absmax, bs, _, shape, bias, gelu_cols, gelu_out) in enumerate(problems):
         n, k = int(shape[0]), int(shape[1])
         gc = int(gelu_cols)
         if len(shape) != 2 or x.shape[-1] != k or not 0 < gc <= n:
             raise ValueError(f"x has {x.shape[-1]} features, weight {tuple(shape)} expects {k}; gelu_cols {gc} "
                              f"must be in (0, {n}]")
+        _check_parts(codec, packed, absmax, n, k, bs)
         x2 = _rows(x)
         if bias is not None and (bias.dtype != x.dtype or not bias.is_contiguous()):
             bias = bias.to(x.dtype).contiguous()
+        _check_bias(bias, n)
         y = torch.empty(*x.shape[:-1], n - gc, dtype=x.dtype, device=dev) if gc < n else None
         if gelu_out is None:
             gelu_out = torch.empty(*x.shape[:-1], gc, dtype=x.dtype, device=dev)
@@ -284,11 +324,13 @@ class GroupedPlan:
         if not self.supported:
             return
         rows_tbl, total_n = [], 0
-        for packed, absmax, _, _, shape, bias in self.weights:
+        for packed, absmax, bs, _, shape, bias in self.weights:
             n = int(shape[0])
+            _check_parts(codec, packed, absmax, n, self.k, 64 if bs is None else bs)
             if bias is not None and (bias.dtype != dtype or not bias.is_contiguous()):
                 bias = bias.to(dtype).contiguous()
                 self._keep.append(bias)
+            _check_bias(bias, n)
             y = torch.empty(self.rows, n, dtype=dtype, device=device)
             self.outs.append(y)
             rows_tbl.append([packed.data_ptr(), absmax.data_ptr(), 0 if bias is None else bias.data_ptr(),
@@ -358,20 +400,44 @@ def _grouped(codec: str, x: torch.Tensor, weights) -> list[torch.Tensor]:
     return [y.view(*x.shape[:-1], y.shape[-1]) for y in outs]
 
 
+_DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16, "uint8": torch.uint8,
+           "int8": torch.int8, "int32": torch.int32, "int64": torch.int64, "float64": torch.float64}
+
+
+def part_view(buf: torch.Tensor, part) -> torch.Tensor:
+    """One part of a unit held in the 1-D uint8 tensor ``buf``, viewed in place with its own dtype and
+    shape (selas/container.py:79-82). ``part`` has selas's PartSpec fields: offset (relative to the
+    unit), nbytes, dtype (a name such as "bfloat16") and shape."""
+    dt = part.dtype if isinstance(part.dtype, torch.dtype) else _DTYPES[str(part.dtype).removeprefix("torch.")]
+    return buf[part.offset: part.offset + part.nbytes].view(dt).view(tuple(part.shape))
+
+
 class UnitView:
     """Typed access to one unit's tensors, as selas.store.UnitView (store.py:242-293).
 
-    ``tensors`` maps tensor names to :class:`EncodedTensor` whose parts live on
-    the GPU. ``get`` decodes (raw tensors in the compute dtype are returned as
-    zero-copy views and cached), ``linear`` is the quantized-linear forward.
+    Built as selas's store builds it, ``UnitView(spec, buf, dtype)``: ``spec`` has ``.tensors``
+    mapping names to TensorSpec-like entries (codec, shape, meta, parts of PartSpec-like entries)
+    and ``buf`` is the unit's 1-D uint8 device buffer; parts are viewed in place (part_view), never
+    copied. ``UnitView(tensors, dtype)`` takes a dict of :class:`EncodedTensor` with device parts
+    instead. ``get`` decodes (raw tensors in the compute dtype are returned as zero-copy views and
+    cached), ``linear`` is the quantized-linear forward.
     """
 
-    __slots__ = ("tensors", "dtype", "_views")
+    __slots__ = ("tensors", "dtype", "_views", "spec", "buf")
 
-    def __init__(self, tensors: dict[str, EncodedTensor], dtype: torch.dtype):
-        self.tensors = tensors
-        self.dtype = dtype
+    def __init__(self, spec_or_tensors, buf_or_dtype, dtype: torch.dtype | None = None):
         self._views: dict[tuple, torch.Tensor] = {}
+        if dtype is None:  # (tensors, dtype)
+            self.spec, self.buf = None, None
+            self.tensors: dict[str, EncodedTensor] = spec_or_tensors
+            self.dtype = buf_or_dtype
+            return
+        self.spec, self.buf, self.dtype = spec_or_tensors, buf_or_dtype, dtype
+        if self.buf.dtype != torch.uint8 or self.buf.dim() != 1:
+            raise ValueError(f"unit buffer must be 1-D uint8, got {self.buf.dtype} {tuple(self.buf.shape)}")
+        self.tensors = {name: EncodedTensor(name, ts.codec, tuple(ts.shape), dict(ts.meta),
+                                            {k: part_view(self.buf, ps) for k, ps in ts.parts.items()})
+                        for name, ts in self.spec.tensors.items()}
 
     def has(self, name: str) -> bool:
         return name in self.tensors

@@ -1,8 +1,9 @@
-"""FLUX blocks on the GPU (fused NF4 linears + segment kernels + SDPA) against the oracle blocks on
-the CPU in fp32 with the same decoded NF4 operands (oracle/flux.py, pinned by reference goldens).
+"""FLUX blocks on the GPU (fused NF4 linears + segment kernels + fused attention) against the oracle blocks
+on the CPU with the same decoded NF4 operands and the reference's bf16 arithmetic (oracle/flux.py, pinned
+by goldens the reference's own functions wrote, in fp32 and in bf16).
 
-Tolerance: the GPU path rounds activations to bf16 between kernels, so block outputs are compared
-on the residual update (out - in): relative L2 <= 2e-2, and the fp32 stream itself <= 4e-3.
+Tolerance: block outputs are compared on the residual update (out - in) at relative L2 <= 4e-3, the
+path's tolerance; the step's velocity likewise.
 """
 
 from __future__ import annotations
@@ -24,9 +25,13 @@ OCFG = OF.FluxConfig(hidden=256, heads=2, mlp_hidden=1024, depth_double=2, depth
                      context_dim=128, vec_dim=64, axes_dim=(16, 56, 56))
 
 
+BF16 = torch.bfloat16
+L2 = 4e-3
+
+
 def oracle_unit(view):
     enc = {n: (e.codec, e.shape, e.meta, {k: v.cpu() for k, v in e.parts.items()}) for n, e in view.tensors.items()}
-    return OF.OracleUnit.from_encoded(enc, torch.float32)
+    return OF.OracleUnit.from_encoded(enc, BF16)
 
 
 def rel(a, b):
@@ -54,9 +59,8 @@ def test_double_block(model):
     dev = torch.device("cuda")
     gi, gt = F.double_block(model.doubles[0], img.to(dev), txt.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG,
                             torch.bfloat16, False)
-    ri, rt = OF.double_block(oracle_unit(model.doubles[0]), img, txt, mod.float(), cos, sin, OCFG, torch.float32, False)
-    assert rel(gi - img.cuda(), ri - img) < 2e-2 and rel(gt - txt.cuda(), rt - txt) < 2e-2
-    assert rel(gi, ri) < 4e-3 and rel(gt, rt) < 4e-3
+    ri, rt = OF.double_block(oracle_unit(model.doubles[0]), img, txt, mod, cos, sin, OCFG, BF16, False)
+    assert rel(gi - img.cuda(), ri - img) < L2 and rel(gt - txt.cuda(), rt - txt) < L2
 
 
 def test_single_block(model):
@@ -66,8 +70,8 @@ def test_single_block(model):
     dev = torch.device("cuda")
     gx = F.single_block(model.singles[0], x.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
                         False)
-    rx = OF.single_block(oracle_unit(model.singles[0]), x, mod.float(), cos, sin, OCFG, torch.float32, False)
-    assert rel(gx - x.cuda(), rx - x) < 2e-2 and rel(gx, rx) < 4e-3
+    rx = OF.single_block(oracle_unit(model.singles[0]), x, mod, cos, sin, OCFG, BF16, False)
+    assert rel(gx - x.cuda(), rx - x) < L2
 
 
 def test_modulations_and_step(model):
@@ -78,28 +82,26 @@ def test_modulations_and_step(model):
     units = [oracle_unit(u) for u in model.mods]
     for i, (m, u) in enumerate(zip(mods, units)):
         if i < len(model.doubles):
-            ref = torch.cat((u.linear(sv.float(), "img_mod.lin"), u.linear(sv.float(), "txt_mod.lin")), dim=-1)
+            ref = torch.cat((u.linear(sv, "img_mod.lin"), u.linear(sv, "txt_mod.lin")), dim=-1)
         else:
-            ref = u.linear(sv.float(), "modulation.lin")
-        assert m.shape == ref.shape and rel(m, ref) < 4e-3
+            ref = u.linear(sv, "modulation.lin")
+        assert m.shape == ref.shape and rel(m, ref) < L2
     img, txt, cos, sin = inputs(1, 64, 8)
     lat = torch.randn(1, 64, 64, generator=seeded(25))
     fmod = (torch.randn(1, 2 * CFG.hidden, generator=seeded(26)) * 0.3).to(torch.bfloat16)
     s = 2
     out = model.step(lat.to(dev), txt.to(dev), [m[s] for m in mods], fmod.to(dev), cos.to(dev), sin.to(dev))
     g = oracle_unit(model.globals)
-    x_img = g.linear(lat.to(torch.bfloat16).float(), "img_in")
+    x_img = g.linear(lat.to(BF16), "img_in").float()
     t = txt
     for i, w in enumerate(model.doubles):
-        x_img, t = OF.double_block(oracle_unit(w), x_img, t, mods[i][s].float().cpu(), cos, sin, OCFG, torch.float32,
-                                   False)
+        x_img, t = OF.double_block(oracle_unit(w), x_img, t, mods[i][s].cpu(), cos, sin, OCFG, BF16, False)
     x = torch.cat((t, x_img), dim=1)
     for j, w in enumerate(model.singles):
-        x = OF.single_block(oracle_unit(w), x, mods[len(model.doubles) + j][s].float().cpu(), cos, sin, OCFG,
-                            torch.float32, False)
-    ref = OF.final_layer(g, x[:, 64:], fmod.float(), torch.float32)
+        x = OF.single_block(oracle_unit(w), x, mods[len(model.doubles) + j][s].cpu(), cos, sin, OCFG, BF16, False)
+    ref = OF.final_layer(g, x[:, 64:], fmod, BF16)
     assert out.shape == (1, 64, 64) and torch.isfinite(out).all()
-    assert rel(out, ref) < 3e-2
+    assert rel(out, ref) < L2
 
 
 def test_batched_step_equals_images_one_by_one(model):
@@ -156,17 +158,17 @@ def test_int8_row_blocks(monkeypatch):
     mod = (torch.randn(2, 12 * CFG.hidden, generator=seeded(30)) * 0.3).to(torch.bfloat16)
     gi, gt = F.double_block(m8.doubles[0], img.to(dev), txt.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG,
                             torch.bfloat16, False)
-    ri, rt = OF.double_block(oracle_unit(m8.doubles[0]), img, txt, mod.float(), cos, sin, OCFG, torch.float32, False)
-    assert rel(gi - img.cuda(), ri - img) < 2e-2 and rel(gt - txt.cuda(), rt - txt) < 2e-2
+    ri, rt = OF.double_block(oracle_unit(m8.doubles[0]), img, txt, mod, cos, sin, OCFG, BF16, False)
+    assert rel(gi - img.cuda(), ri - img) < L2 and rel(gt - txt.cuda(), rt - txt) < L2
     x = torch.cat((txt, img), dim=1)
     smod = (torch.randn(2, 3 * CFG.hidden, generator=seeded(31)) * 0.3).to(torch.bfloat16)
     gx = F.single_block(m8.singles[0], x.to(dev), smod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16, False)
-    rx = OF.single_block(oracle_unit(m8.singles[0]), x, smod.float(), cos, sin, OCFG, torch.float32, False)
-    assert rel(gx - x.cuda(), rx - x) < 2e-2 and rel(gx, rx) < 4e-3
+    rx = OF.single_block(oracle_unit(m8.singles[0]), x, smod, cos, sin, OCFG, BF16, False)
+    assert rel(gx - x.cuda(), rx - x) < L2
     sv = torch.nn.functional.silu(torch.randn(5, 1, CFG.hidden, generator=seeded(32))).to(torch.bfloat16)
     mods = m8.modulations(sv.to(dev))
     u = oracle_unit(m8.mods[1])
-    assert rel(mods[1], u.linear(sv.float(), "modulation.lin")) < 4e-3
+    assert rel(mods[1], u.linear(sv, "modulation.lin")) < L2
     fused = F.single_block(m8.singles[0], x.to(dev), smod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
                            False)
     monkeypatch.setattr(F, "_fused_gelu", lambda w, k: False)
@@ -191,11 +193,10 @@ def test_blocks_at_a_token_count_off_the_tiles(model):
     mod = (torch.randn(1, 3 * CFG.hidden, generator=seeded(33)) * 0.3).to(torch.bfloat16)
     gx = F.single_block(model.singles[1], x.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG, torch.bfloat16,
                         False)
-    rx = OF.single_block(oracle_unit(model.singles[1]), x, mod.float(), cos, sin, OCFG, torch.float32, False)
-    assert rel(gx - x.cuda(), rx - x) < 2e-2 and rel(gx, rx) < 4e-3
+    rx = OF.single_block(oracle_unit(model.singles[1]), x, mod, cos, sin, OCFG, BF16, False)
+    assert rel(gx - x.cuda(), rx - x) < L2
     dmod = (torch.randn(1, 12 * CFG.hidden, generator=seeded(34)) * 0.3).to(torch.bfloat16)
     gi, gt = F.double_block(model.doubles[1], img.to(dev), txt.to(dev), dmod.to(dev), cos.to(dev), sin.to(dev), CFG,
                             torch.bfloat16, False)
-    ri, rt = OF.double_block(oracle_unit(model.doubles[1]), img, txt, dmod.float(), cos, sin, OCFG, torch.float32,
-                             False)
-    assert rel(gi - img.cuda(), ri - img) < 2e-2 and rel(gt - txt.cuda(), rt - txt) < 2e-2
+    ri, rt = OF.double_block(oracle_unit(model.doubles[1]), img, txt, dmod, cos, sin, OCFG, BF16, False)
+    assert rel(gi - img.cuda(), ri - img) < L2 and rel(gt - txt.cuda(), rt - txt) < L2

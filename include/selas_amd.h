@@ -210,6 +210,28 @@ int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx, c
                              int64_t count, int64_t total_n, int64_t blocksize, const float code[16], int dtype,
                              void *stream);
 
+/* At most this many weights per selas_nf4_linear_grouped_static call. */
+#define SELAS_STATIC_MAX_WEIGHTS 1023
+
+/*
+ * selas_nf4_linear_grouped that allocates nothing and needs no device memory of
+ * the caller's beyond x, the weights, biases and outputs: `descs` is an array
+ * of `count` descriptors in HOST memory (read during the call only), and the
+ * sum of their n is computed here. The library stages the descriptors in a
+ * device table of its own, SELAS_STATIC_MAX_WEIGHTS * 48 bytes (49,104 bytes)
+ * per GPU, held until the process ends; count above SELAS_STATIC_MAX_WEIGHTS
+ * is rejected with SELAS_EINVAL. Every call on a GPU rewrites that table before
+ * its kernels read it, so calls on one stream are ordered, but calls that
+ * overlap on one GPU (on different streams, or from threads that do not
+ * order them) race on it. Each output has the bits selas_nf4_linear_grouped
+ * (and selas_nf4_linear) gives for that weight.
+ * No counterpart in the reference. It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, serving loops with a fixed
+ * memory budget, harnesses that forbid hipMalloc.
+ */
+int selas_nf4_linear_grouped_static(const void *x, int64_t M, int64_t K, int64_t ldx, const selas_nf4_gemv_desc *descs,
+                                    int64_t count, int64_t blocksize, const float code[16], int dtype, void *stream);
+
 /*
  * selas_nf4_linear_grouped for int8_row weights (M <= 32, K = 1024, 2048 or
  * 3072, bf16): in each descriptor `packed` holds q [n, K] (16-byte aligned) and

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libselas_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
     "selas_nf4_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _F16x, _I64, _P, _P, _I64, _INT, _P],
     "selas_nf4_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F16x, _INT, _P],
     "selas_nf4_linear_batched": [_P, _I64, _I64, _F16x, _INT, _P],
+    "selas_nf4_linear_grouped_static": [_P, _I64, _I64, _I64, _P, _I64, _I64, _F16x, _INT, _P],
     "selas_int8_row_dequant": [_P, _P, _I64, _I64, _P, _INT, _P],
     "selas_int8_row_encode": [_P, _I64, _I64, _P, _P, _P],
     "selas_int8_row_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _INT, _P],
@@ -57,6 +58,15 @@ class GemmProblem(ctypes.Structure):
 
     _fields_ = [("x", _P), ("M", _I64), ("K", _I64), ("ldx", _I64), ("packed", _P), ("absmax", _P), ("N", _I64),
                 ("bias", _P), ("y", _P), ("ldy", _I64), ("y2", _P), ("ldy2", _I64), ("gelu_cols", _I64)]
+
+
+class GemvDesc(ctypes.Structure):
+    """selas_nf4_gemv_desc (include/selas_amd.h): one weight of a grouped skinny launch."""
+
+    _fields_ = [("packed", _P), ("absmax", _P), ("bias", _P), ("y", _P), ("n", _I64), ("ldy", _I64)]
+
+
+STATIC_MAX_WEIGHTS = 1023
 
 
 class Unsupported(NotImplementedError):

@@ -25,6 +25,10 @@
 // [32h, 32h+32) and sub-step s covers k in [32h+8s, 32h+8s+8), so one 16-byte
 // load of packed codes feeds a lane for a whole 64-block. The 32x32 fp32
 // result has, in lane l, column l%32 and rows 8*(r/4) + 4*h + r%4, r = 0..15.
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+
 #include "common.h"
 
 namespace selas {
@@ -1705,4 +1709,110 @@ extern "C" int selas_int8_row_linear_grouped(const void *x, int64_t M, int64_t K
   const GemvDesc none{nullptr, nullptr, nullptr, nullptr, 0, 0};
   return launch_i8_gemv_stream(static_cast<const uint16_t *>(x), ldx, M, K, reinterpret_cast<const GemvDesc *>(descs),
                                static_cast<int>(count), none, total_n, static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------ grouped skinny GEMM without caller memory
+//
+// selas_nf4_linear_grouped reads its weight descriptors from a device array the
+// caller allocates. This variant takes them in host memory and stages them in a
+// descriptor table of the library's own: `scratch`, a device array of the code
+// object (one copy per GPU, held until the process ends). Its device address
+// comes from hipGetSymbolAddress once per device, on the first call there, and
+// only that address is passed to kernels: the array's name in host code is a
+// host-side stand-in, not a device address. The descriptors reach it as kernel
+// arguments of a small copy kernel (kStageDescs per launch), so no copy from
+// host memory and no allocation is made. Every call on a GPU rewrites the
+// table before reading it; calls that overlap on one GPU (different streams)
+// race on it.
+namespace {
+constexpr int kStaticDescs = kSgMaxDescs;  // 1023 descriptors, 49,104 bytes
+constexpr int kStageDescs = 64;            // descriptors per copy launch (3,072 bytes of arguments)
+constexpr int kMaxDevices = 64;
+static_assert(kStaticDescs == SELAS_STATIC_MAX_WEIGHTS, "scratch size");
+
+__device__ __align__(256) GemvDesc scratch[kStaticDescs];
+
+struct DescChunk {
+  GemvDesc d[kStageDescs];
+  int first, count;
+};
+
+// Thread i copies descriptor i of the chunk to dst[first + i] (vector stores).
+__global__ __launch_bounds__(kStageDescs) void stage_descs(DescChunk c, GemvDesc *dst) {
+  const int i = threadIdx.x;
+  if (i < c.count) dst[c.first + i] = c.d[i];
+}
+
+std::mutex scratch_mu;
+GemvDesc *scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device (resolved once per device).
+int scratch_table(GemvDesc **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(SELAS_EHIP, "nf4_linear_grouped_static: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(SELAS_EHIP, "nf4_linear_grouped_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    scratch_ptr[dev] = static_cast<GemvDesc *>(p);
+  }
+  *out = scratch_ptr[dev];
+  return SELAS_OK;
+}
+}  // namespace
+
+extern "C" int selas_nf4_linear_grouped_static(const void *x, int64_t M, int64_t K, int64_t ldx,
+                                               const selas_nf4_gemv_desc *descs, int64_t count, int64_t blocksize,
+                                               const float code[16], int dtype, void *stream) {
+  if (M < 0 || K <= 0 || count < 0)
+    return set_error(SELAS_EINVAL, "nf4_linear_grouped_static: bad shape M=%lld K=%lld count=%lld", (long long)M,
+                     (long long)K, (long long)count);
+  if (count > kStaticDescs)
+    return set_error(SELAS_EINVAL, "nf4_linear_grouped_static: %lld weights, at most %d (SELAS_STATIC_MAX_WEIGHTS)",
+                     (long long)count, kStaticDescs);
+  if (M == 0 || count == 0) return ok();
+  if (!x || !descs || !code) return set_error(SELAS_EINVAL, "nf4_linear_grouped_static: null pointer");
+  if (ldx < K) return set_error(SELAS_EINVAL, "nf4_linear_grouped_static: ldx below K");
+  if (dtype != SELAS_BF16) return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: takes bf16");
+  if (blocksize != 64 || !stream_k(K) || M > 32)
+    return set_error(SELAS_EUNSUPPORTED,
+                     "nf4_linear_grouped_static: needs blocksize 64, K = 1024, 2048 or 3072 and M <= 32");
+  if (!aligned(x, 16) || ldx % 8)
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: x rows must be 16-byte aligned");
+  int64_t total_n = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const selas_nf4_gemv_desc &d = descs[i];
+    if (d.n <= 0 || d.ldy < d.n || !d.packed || !d.absmax || !d.y)
+      return set_error(SELAS_EINVAL, "nf4_linear_grouped_static: descriptor %lld: n=%lld ldy=%lld or a null pointer",
+                       (long long)i, (long long)d.n, (long long)d.ldy);
+    if (!aligned(d.packed, 16) || !aligned(d.absmax, 4) || !aligned(d.y, 2) || (d.bias && !aligned(d.bias, 2)))
+      return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: descriptor %lld: misaligned codes or output",
+                       (long long)i);
+    if (d.n * (K / 2) >= (1ll << 32) || M * d.ldy * 2 >= (1ll << 32))
+      return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: descriptor %lld: a weight above 4 GiB",
+                       (long long)i);
+    total_n += d.n;
+  }
+  GemvDesc *table = nullptr;
+  if (int e = scratch_table(&table)) return e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int64_t first = 0; first < count; first += kStageDescs) {
+    DescChunk chunk{};
+    chunk.first = static_cast<int>(first);
+    chunk.count = static_cast<int>(std::min<int64_t>(kStageDescs, count - first));
+    std::memcpy(chunk.d, descs + first, sizeof(GemvDesc) * chunk.count);
+    stage_descs<<<dim3(1), dim3(kStageDescs), 0, s>>>(chunk, table);
+    if (int e = check_launch("nf4_linear_grouped_static (descriptor copy)")) return e;
+  }
+  Code16 c;
+  for (int i = 0; i < 16; ++i) c.v[i] = code[i];
+  const GemvDesc none{nullptr, nullptr, nullptr, nullptr, 0, 0};
+  return launch_gemv_stream(static_cast<const uint16_t *>(x), ldx, M, K, table, static_cast<int>(count), none, total_n,
+                            c, s);
 }

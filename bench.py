@@ -9,8 +9,9 @@ above the 256 MB Infinity Cache).
 The same JSON line carries:
   roofline      the fused GEMM kernel's FLOP/s from HIP-event durations of its launches
                 against the 2.5 PFLOP/s dense bf16 MFMA peak;
-  cpu_baseline  the reference's dequantize-then-torch path (the oracle's C decode + torch
-                F.linear in fp32) on the host cores, on a bounded row sample;
+  cpu_baseline  the reference's dequantize-then-torch path (the oracle's restatement of the torch
+                NF4 decode + torch F.linear) on the host cores for the same two linears, the faster
+                of fp32 and bf16; extra.cpu_baselines has every configuration (C1-C5) in both;
   extra         the other configurations: the 1536-token single linear, the 76 hoisted
                 modulation GEMMs at M = 28 (HBM-bound, GB/s), the fused segments at M = 4608
                 (GB/s), the library dequant + hipBLASLt path on the GPU for comparison, the fused
@@ -506,45 +507,152 @@ def bench_full_step(dev, steps, warmup, batch=1, res=1024):
 # --------------------------------------------------------------------------- CPU baseline
 
 
-def cpu_baseline(target_s: float = 12.0):
-    """Dequantize-then-F.linear on the host for one block's two linears at M = 4608 (fp32, all cores).
+class CpuRefUnit:
+    """The reference's CPU linear for one unit: every NF4 weight decoded on each call by the torch decode
+    (selas/codecs.py:178-199, restated in the oracle) into the compute dtype, then F.linear in that dtype
+    (selas/store.py:289-293). Parts are uniformly random codes and absmax: neither the decode's nor the
+    GEMM's time depends on the values."""
 
-    The weights are decoded by the oracle's C restatement of the reference decode; the GEMM runs on a
-    row sample sized to about `target_s` seconds and the full-step time is extrapolated linearly in rows."""
-    import numpy as np
+    def __init__(self, shapes: dict, dt, seed: int):
+        g = torch.Generator().manual_seed(seed)
+        self.dt, self.w = dt, {}
+        for name, (n, k) in shapes.items():
+            packed = torch.randint(0, 256, (n * k // 2,), generator=g, dtype=torch.uint8)
+            absmax = torch.rand(n * k // 64, generator=g) * 0.08 + 0.02
+            bias = (torch.randn(n, generator=g) * 0.02).to(dt)
+            self.w[name] = (packed, absmax, (n, k), bias)
+        self.norms = {}
 
-    from oracle import nf4 as onf4
+    def get(self, name, dtype=None):
+        return self.norms.setdefault(name, torch.ones(128)).to(dtype or self.dt)
+
+    def linear(self, x, prefix, dtype=None):
+        from oracle import nf4 as onf4
+
+        dt = dtype or self.dt
+        packed, absmax, shape, bias = self.w[prefix]
+        w = onf4.decode_torch(packed, absmax, 64, onf4.NF4_CODE, shape, dt)
+        return torch.nn.functional.linear(x.to(dt), w, bias)
+
+
+def _sdpa_cpu(q, k, v):
+    """The reference's attention call (flux.py:135-138) on the CPU."""
+    b, h, l, d = q.shape
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(b, l, h * d)
+
+
+def _timed(fn, reps: int = 1) -> float:
+    fn()  # first call outside the timing (allocator, thread pool)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+def _rows_timed(run, total_rows: int, budget_s: float) -> tuple[float, int]:
+    """Seconds for `run(rows)` at `total_rows`: timed in full when a 1/16 sample projects under
+    `budget_s`, otherwise extrapolated linearly from the largest sample timed."""
+    rows = max(1, total_rows // 16)
+    t = _timed(lambda: run(rows))
+    if t * total_rows / rows <= budget_s:
+        return _timed(lambda: run(total_rows)), total_rows
+    return t * total_rows / rows, rows
+
+
+def cpu_baselines(budget_s: float = 6.0):
+    """The reference's CPU path (dequantize-then-torch: the torch NF4 decode + F.linear, the eager segments)
+    for every configuration, in fp32 and in bf16, on all host cores. C1-C3 are timed in full when that
+    fits `budget_s` per run (otherwise on a row sample, extrapolated in rows); C4 on 4 of the 38 weights
+    of each shape, extrapolated x38/4; C5 from one double and one single block at full shape plus img_in
+    and the final layer, extrapolated x19 / x38."""
+    from oracle import flux as OF
+    from oracle import segments as S
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    rng = np.random.default_rng(0)
-    shapes = [(3 * D + MLP, D), (D, D + MLP)]
-    dec_s, gemm_s_per_row = 0.0, 0.0
-    rows_used = 0
-    for n, k in shapes:
-        w = (rng.standard_normal((n, k), dtype=np.float32) * 0.02)
-        p, a = onf4.c_encode(w) if onf4.c_lib() else onf4.encode(w)
-        del w
-        t0 = time.perf_counter()
-        wd = onf4.c_decode(p, a, 64) if onf4.c_lib() else onf4.decode(p, a, 64)
-        dec_s += time.perf_counter() - t0
-        wt = torch.from_numpy(wd).view(n, k)
-        rows = 64
-        while True:
-            x = torch.randn(rows, k)
-            t0 = time.perf_counter()
-            torch.nn.functional.linear(x, wt)
-            dt = time.perf_counter() - t0
-            if dt > target_s / 4 or rows >= M_1024:
-                break
-            rows = min(M_1024, rows * 4)
-        gemm_s_per_row += dt / rows
-        rows_used = max(rows_used, rows)
-    step_s = dec_s + gemm_s_per_row * M_1024
-    f = 2.0 * M_1024 * ((3 * D + MLP) * D + D * (D + MLP))
-    return {"value": f / step_s / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"oracle C decode of both weights + torch fp32 F.linear on {rows_used}-row samples, "
-                      f"extrapolated to 4608 rows: {step_s:.2f} s per step ({dec_s:.2f} s decode)"}
+    g = torch.Generator().manual_seed(0)
+    out = {"cores": threads, "configs": {}}
+    f32, bf16 = torch.float32, torch.bfloat16
+    for dt in (f32, bf16):
+        key = "fp32" if dt == f32 else "bf16"
+        log(f"bench: cpu baseline {key}")
+        res = {}
+        # C1: 1536 x 12288 x 3072
+        u = CpuRefUnit({"w": (4 * D, D)}, dt, 1)
+        x = torch.randn(1536, D, generator=g).to(dt)
+        t, rows = _rows_timed(lambda r: u.linear(x[:r], "w"), 1536, budget_s)
+        res["c1_single_linear_1536"] = {"s": t, "tflops": 2.0 * 1536 * 4 * D * D / t / 1e12, "rows_timed": rows}
+        # C2: linear1 + linear2 at M = 4608
+        u = CpuRefUnit({"linear1": (3 * D + MLP, D), "linear2": (D, D + MLP)}, dt, 2)
+        x1 = torch.randn(M_1024, D, generator=g).to(dt)
+        x2 = torch.randn(M_1024, D + MLP, generator=g).to(dt)
+        t1, r1 = _rows_timed(lambda r: u.linear(x1[:r], "linear1"), M_1024, budget_s)
+        t2, r2 = _rows_timed(lambda r: u.linear(x2[:r], "linear2"), M_1024, budget_s)
+        f2 = 2.0 * M_1024 * ((3 * D + MLP) * D + D * (D + MLP))
+        res["c2_block_linears_1024"] = {"s": t1 + t2, "tflops": f2 / (t1 + t2) / 1e12, "rows_timed": [r1, r2]}
+        # C3: the eager segments at M = 4608 (bytes as counted for the GPU kernels)
+        xs = torch.randn(1, M_1024, D, generator=g)
+        mod = torch.randn(1, 3 * D, generator=g) * 0.1
+        sh, sc, gate = mod.unsqueeze(1).chunk(3, dim=-1)
+        h = torch.randn(1, M_1024, 3 * D + MLP, generator=g).to(dt)
+        qs, ks = 1 + 0.02 * torch.randn(128, generator=g), 1 + 0.02 * torch.randn(128, generator=g)
+        ang = torch.rand(M_1024, 64, generator=g, dtype=torch.float64) * 50
+        cos, sin = ang.cos().float(), ang.sin().float()
+        y = torch.randn(1, M_1024, D, generator=g).to(dt)
+        attn = torch.randn(1, M_1024, D, generator=g).to(dt)
+        seg = {"mod_in": (lambda: S.mod_in(xs, sh, sc, dt), M_1024 * D * 6 + 2 * D * 4),
+               "qkv_single": (lambda: S.qkv_single(h[..., :3 * D], qs, ks, cos, sin, 24, dt),
+                              M_1024 * 3 * D * 2 * 2 + 2 * M_1024 * 64 * 4),
+               "gated_add": (lambda: S.gated_add(xs, gate, y, False), M_1024 * D * 10 + D * 4),
+               "attn_mlp": (lambda: S.attn_mlp(attn, h[..., 3 * D:]), M_1024 * (D + MLP) * 4)}
+        res["c3_segments_4608"] = {}
+        for name, (fn, nb) in seg.items():
+            t = _timed(fn, 2)
+            res["c3_segments_4608"][name] = {"s": t, "gbs": nb / t / 1e9}
+        # C4: 76 modulation linears at M = 28 (4 weights of each shape timed)
+        sv = torch.nn.functional.silu(torch.randn(28, D, generator=g)).to(dt)
+        ud = CpuRefUnit({f"d{i}": (6 * D, D) for i in range(4)}, dt, 3)
+        us = CpuRefUnit({f"s{i}": (3 * D, D) for i in range(4)}, dt, 4)
+        td = _timed(lambda: [ud.linear(sv, f"d{i}") for i in range(4)])
+        ts = _timed(lambda: [us.linear(sv, f"s{i}") for i in range(4)])
+        t4 = (td + ts) * 38 / 4
+        nb4 = 1876586496
+        res["c4_modulations_m28"] = {"s": t4, "gbs": nb4 / t4 / 1e9, "sample": "4 + 4 of 38 + 38 weights"}
+        # C5: one double + one single block at 1024^2 (B1), img_in and the final layer; x19 / x38
+        cfg = OF.FluxConfig()
+        dshapes = {}
+        for st in ("img", "txt"):
+            dshapes.update({f"{st}_attn.qkv": (3 * D, D), f"{st}_attn.proj": (D, D), f"{st}_mlp.0": (MLP, D),
+                            f"{st}_mlp.2": (D, MLP)})
+        du = CpuRefUnit(dshapes, dt, 5)
+        su = CpuRefUnit({"linear1": (3 * D + MLP, D), "linear2": (D, D + MLP)}, dt, 6)
+        gu = CpuRefUnit({"img_in": (D, 64), "final_layer.linear": (64, D)}, dt, 7)
+        img = torch.randn(1, 4096, D, generator=g)
+        txt = torch.randn(1, 512, D, generator=g)
+        xs5 = torch.cat((txt, img), dim=1)
+        ids = torch.cat((torch.zeros(512, 3), torch.stack(torch.meshgrid(torch.zeros(1), torch.arange(64.0),
+                                                                          torch.arange(64.0), indexing="ij"),
+                                                           -1).reshape(-1, 3)), dim=0)
+        cos5, sin5 = S.rope_tables(ids, cfg.axes_dim, cfg.theta)
+        dmod = (torch.randn(1, 12 * D, generator=g) * 0.1).to(dt)
+        smod = (torch.randn(1, 3 * D, generator=g) * 0.1).to(dt)
+        fmod = (torch.randn(1, 2 * D, generator=g) * 0.1).to(dt)
+        lat = torch.randn(1, 4096, 64, generator=g)
+        guard = dt == torch.float16
+        k = S.OracleKernels
+        tdb = _timed(lambda: OF.double_block(du, img, txt, dmod, cos5, sin5, cfg, dt, guard, k, _sdpa_cpu))
+        tsb = _timed(lambda: OF.single_block(su, xs5, smod, cos5, sin5, cfg, dt, guard, k, _sdpa_cpu))
+        tgl = _timed(lambda: (gu.linear(lat.to(dt), "img_in"), OF.final_layer(gu, img, fmod, dt, k)))
+        t5 = 19 * tdb + 38 * tsb + tgl
+        res["c5_full_step_1024_b1"] = {"s_per_step": t5, "double_block_s": tdb, "single_block_s": tsb,
+                                       "globals_s": tgl, "tflops": 74.36e12 / t5 / 1e12,
+                                       "sample": "one double + one single block at full shape, x19 / x38"}
+        out["configs"][key] = res
+    best = max(out["configs"].values(), key=lambda r: r["c2_block_linears_1024"]["tflops"])
+    out["c2_best"] = {"value": best["c2_block_linears_1024"]["tflops"],
+                      "dtype": "fp32" if best is out["configs"]["fp32"] else "bf16"}
+    out["c5_best_s_per_step"] = min(r["c5_full_step_1024_b1"]["s_per_step"] for r in out["configs"].values())
+    return out
 
 
 # --------------------------------------------------------------------------- HBM traffic
@@ -600,11 +708,17 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     log(f"bench: {torch.cuda.get_device_name(dev)}")
+    # The host-only CPU baselines run first, while the GPU is idle anyway; the GPU work follows, with the
+    # headline measurement last, so that it runs on a GPU past its clock ramp under sustained load.
+    cpu_all = None if a.no_cpu else cpu_baselines()
+    if cpu_all is not None:
+        for key, r in cpu_all["configs"].items():
+            log(f"bench: cpu {key} on {cpu_all['cores']} cores: C1 {r['c1_single_linear_1536']['tflops']:.2f} "
+                f"TFLOP/s, C2 {r['c2_block_linears_1024']['tflops']:.2f} TFLOP/s, C4 "
+                f"{r['c4_modulations_m28']['gbs']:.1f} GB/s, C5 {r['c5_full_step_1024_b1']['s_per_step']:.1f} s/step")
     if a.traffic_calibration:
         copy_calibration(dev)
-    res = bench_block_linears(dev, a.steps, a.warmup)
-    log(f"bench: block linears {res['kernel_tflops']}")
-    extra = {"block_linears": res}
+    extra = {}
     if not a.no_extra:
         extra["single_linear_1536"] = bench_single_linear(dev, a.steps, a.warmup)
         log(f"bench: single linear {extra['single_linear_1536']['tflops']:.1f} TFLOP/s")
@@ -630,7 +744,23 @@ def main():
             r = extra[key]
             log(f"bench: full step B{batch} at {res_px}^2: {r['s_per_step']:.4f} s/step "
                 f"(lower bound {r['lower_bound_s']:.4f} s, {100 * r['frac_of_bound']:.0f} %)")
-    cpu = None if a.no_cpu else cpu_baseline()
+        if cpu_all is not None:
+            fs = extra["full_step_1024_b1"]
+            fs["cpu_s_per_step"] = cpu_all["c5_best_s_per_step"]
+            fs["speedup_vs_cpu"] = cpu_all["c5_best_s_per_step"] / fs["s_per_step"]
+            log(f"bench: full step B1 at 1024^2: {fs['s_per_step']:.4f} s/step on the GPU, "
+                f"{fs['cpu_s_per_step']:.1f} s/step on {cpu_all['cores']} CPU cores")
+    res = bench_block_linears(dev, a.steps, a.warmup)
+    log(f"bench: block linears {res['kernel_tflops']}")
+    extra["block_linears"] = res
+    cpu = None
+    if cpu_all is not None:
+        extra["cpu_baselines"] = cpu_all
+        cpu = {"value": cpu_all["c2_best"]["value"], "unit": "TFLOP/s", "cores": cpu_all["cores"], "kind": "port",
+               "sample": f"the reference's dequantize-then-F.linear path on the host (the oracle's restatement of "
+                         f"the torch NF4 decode, torch F.linear) for linear1 + linear2 at M = 4608, "
+                         f"{cpu_all['c2_best']['dtype']} (the faster of fp32 and bf16), all rows; every config "
+                         f"in extra.cpu_baselines"}
     achieved = res["achieved_tflops"]
     line = {
         "metric": METRIC,

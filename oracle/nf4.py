@@ -150,3 +150,30 @@ def c_encode(w: np.ndarray, blocksize: int = 64, code=NF4_CODE) -> tuple[np.ndar
     if lib.nf4o_encode(_p(flat), flat.size, blocksize, _p(c), _p(packed), _p(absmax)):
         raise ValueError(f"nf4 needs numel divisible by blocksize ({flat.size} % {blocksize})")
     return packed, absmax
+
+
+# --------------------------------------------------------------------------- torch restatement (CPU baseline)
+
+
+def decode_torch(packed, absmax, blocksize: int, code, shape, dtype, chunk_bytes: int = 1 << 23):
+    """The reference's torch decode on the CPU (selas/codecs.py:155-199): a [256, 2] fp32 table maps a byte
+    to (code[hi], code[lo]); rows of a blocksize-wide view are multiplied by their absmax in fp32 and
+    copied (rounded once) into the output, 8 MiB of codes at a time. The same values as ``decode``; this
+    is the path the benchmark times as the reference's CPU linear."""
+    import torch
+
+    packed = torch.as_tensor(packed).reshape(-1)
+    absmax = torch.as_tensor(absmax).reshape(-1)
+    n_bytes = packed.numel()
+    out = torch.empty(n_bytes * 2, dtype=dtype)
+    c = torch.tensor([float(v) for v in code], dtype=torch.float32)
+    b = torch.arange(256)
+    lut = torch.stack((c[b >> 4], c[b & 15]), dim=1)
+    bpb = blocksize // 2
+    step = max(bpb, (chunk_bytes // bpb) * bpb)
+    for s in range(0, n_bytes, step):
+        e = min(n_bytes, s + step)
+        vals = lut.index_select(0, packed[s:e].to(torch.int32)).view(-1, blocksize)
+        vals.mul_(absmax[s // bpb:e // bpb].unsqueeze(1))
+        out[2 * s:2 * e].copy_(vals.view(-1))
+    return out.view(tuple(shape))

@@ -128,3 +128,20 @@ def test_encode_rejects_partial_blocks():
         nf4.encode(np.zeros(100, dtype=np.float32), 64)
     with pytest.raises(ValueError):
         nf4.encode(np.zeros(63, dtype=np.float32), 3)
+
+
+def test_torch_restatement_equals_the_c_and_numpy_decodes():
+    # The torch decode the benchmark times as the reference's CPU path gives the bits of the pinned decodes,
+    # across chunk boundaries (chunk of 96 bytes over a 1000-byte tensor) and for every output type.
+    import torch
+
+    rng = np.random.default_rng(5)
+    packed = rng.integers(0, 256, 1024, dtype=np.uint8)
+    absmax = (rng.random(32, dtype=np.float32) * 3).astype(np.float32)
+    absmax[3] = 0.0
+    for dt, out in ((torch.float32, nf4.F32), (torch.float16, nf4.F16), (torch.bfloat16, nf4.BF16)):
+        got = nf4.decode_torch(packed, absmax, 64, nf4.NF4_CODE, (2048,), dt, chunk_bytes=96)
+        want = nf4.decode(packed, absmax, 64, out=out)
+        bits = got.view(torch.int32 if dt == torch.float32 else torch.int16).numpy()
+        assert (bits.view(np.uint32 if dt == torch.float32 else np.uint16) == want.view(bits.dtype).view(
+            np.uint32 if dt == torch.float32 else np.uint16)).all()

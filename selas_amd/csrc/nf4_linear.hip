@@ -315,14 +315,8 @@ __global__ __launch_bounds__(kI8GemvThreads, 4) void int8_row_gemv_kernel(
 constexpr int kSgRows = 32;
 constexpr int kSgTableBytes = 256 * 64 * 4;  // [byte][lane] -> fp16 code pair
 constexpr int kSgMaxDescs = 1023;
-#ifndef SG_AHEAD
-#define SG_AHEAD 1
-#endif
-constexpr int kSgAhead = SG_AHEAD;  // sub-steps of table lookups in flight
-#ifndef SG_WAVES
-#define SG_WAVES 8
-#endif
-constexpr int kSgWaves = SG_WAVES;  // waves per workgroup (8: two per SIMD; 4 measured 25 % slower)
+constexpr int kSgAhead = 1;  // sub-steps of table lookups in flight
+constexpr int kSgWaves = 8;  // waves per workgroup (8: two per SIMD; 4 measured 25 % slower)
 
 template <int NW, int BPW>
 struct SgLayout {

@@ -550,12 +550,18 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     const float bv = bf16_bits_to_f32(static_cast<uint16_t>(bias_bits));
     const auto ry = make_rsrc(d.y, static_cast<uint32_t>(((M - 1) * d.ldy + N) * 2));
     const float *rb = red + buf * NW * 1024;
+    // All partials first (one batch of LDS reads), then the sums in wave order.
+    float part[L::kOuts][NW];
+#pragma unroll
+    for (int i = 0; i < L::kOuts; ++i)
+#pragma unroll
+      for (int w = 0; w < NW; ++w) part[i][w] = rb[w * 1024 + tid + kThreads * i];
 #pragma unroll
     for (int i = 0; i < L::kOuts; ++i) {
       const int e = tid + kThreads * i;
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) v += rb[w * 1024 + e];
+      for (int w = 0; w < NW; ++w) v += part[i][w];
       const int r = e >> 6;
       const int m = 8 * (r >> 2) + 4 * h + (r & 3);
       const int n = row0 + c;
@@ -619,10 +625,13 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     uint32_t ebuf[kSgAhead + 1][4];
 #pragma unroll
     for (int t = 0; t < kSgAhead; ++t) lookup(word(t), ebuf[t]);
+    // Block b's sums go to p[b & 1]; they are scaled into acc after block b+1's second MFMA,
+    // when the MFMA results are ready, so the wave does not wait for them.
     f32x16 acc = f32x16{};
+    f32x16 p[2];
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
-      f32x16 p = f32x16{};
+      p[b & 1] = f32x16{};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int t = 4 * b + s;
@@ -630,12 +639,16 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
         // Keep those reads ahead of this sub-step's MFMAs (the scheduler would sink them to their use).
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t(&e)[4] = ebuf[t % (kSgAhead + 1)];
-        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[b][s], __builtin_bit_cast(f16x8, make_uint4(e[0], e[1], e[2], e[3])),
-                                                   p, 0, 0, 0);
-      }
+        p[b & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            xf[b][s], __builtin_bit_cast(f16x8, make_uint4(e[0], e[1], e[2], e[3])), p[b & 1], 0, 0, 0);
+        if (s == 1 && b > 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] += p[r] * a[b];
+          for (int r = 0; r < 16; ++r) acc[r] += p[(b - 1) & 1][r] * a[b - 1];
+        }
+      }
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += p[(BPW - 1) & 1][r] * a[BPW - 1];
     wait_vmcnt<0>();  // this wave's DMAs of unit u+1 have landed
     float *rw = red + buf * NW * 1024;
     if constexpr (L::kRedBufs == 1) {

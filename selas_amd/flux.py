@@ -95,6 +95,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
         return out
 
 
+# RandomFlux.step runs each block's closing residual add together with the next block's mod_in
+# (gated_add_mod) when the two blocks are of one kind.
+CHAIN_BLOCKS = True
+
+
 def _fused_gelu(w, k) -> bool:
     """The GELU after the MLP input linears goes into the GEMM epilogue when the unit can do that and the
     segments are this package's kernels (whose GELU the epilogue reproduces bit for bit)."""
@@ -112,15 +117,23 @@ def _linear_pair(w, a, b):
     return ya, yb
 
 
-def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kernels = FUSED):
-    """img [B, Li, D] fp32, txt [B, Lt, D] fp32, mod [B, 12D] (img 6D | txt 6D)."""
+def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kernels = FUSED, h=None,
+                 next_mod=None):
+    """img [B, Li, D] fp32, txt [B, Lt, D] fp32, mod [B, 12D] (img 6D | txt 6D).
+
+    ``h``: the (img, txt) inputs of the attention linears, mod_in of img and txt with this block's first
+    shift and scale, when the previous block computed them. With ``next_mod`` (the next double block's
+    [B, 12D]) the closing residual adds also compute the next block's ``h`` in the same pass
+    (gated_add_mod) and the result is ``(img, txt, h_next)``."""
     m = mod.float().unsqueeze(1).chunk(12, dim=-1)
     i_sh1, i_sc1, i_g1, i_sh2, i_sc2, i_g2 = m[:6]
     t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = m[6:]
     lt = txt.shape[1]
     f32 = torch.float32
-    iqkv, tqkv = _linear_pair(w, (k.mod_in(img, i_sh1, i_sc1, dt), "img_attn.qkv"),
-                              (k.mod_in(txt, t_sh1, t_sc1, dt), "txt_attn.qkv"))
+    if h is None:
+        h = (k.mod_in(img, i_sh1, i_sc1, dt), k.mod_in(txt, t_sh1, t_sc1, dt))
+    iqkv, tqkv = _linear_pair(w, (h[0], "img_attn.qkv"), (h[1], "txt_attn.qkv"))
+    del h
     q, kk, v = k.qkv_double(tqkv, iqkv, w.get("txt_attn.norm.query_norm.scale", f32),
                             w.get("txt_attn.norm.key_norm.scale", f32), w.get("img_attn.norm.query_norm.scale", f32),
                             w.get("img_attn.norm.key_norm.scale", f32), cos, sin, cfg.heads, dt)
@@ -140,21 +153,41 @@ def double_block(w, img, txt, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k
         hi, ht = _linear_pair(w, (hi, "img_mlp.0"), (ht, "txt_mlp.0"))
         hi, ht = k.gelu(hi), k.gelu(ht)
     oi, ot = _linear_pair(w, (hi, "img_mlp.2"), (ht, "txt_mlp.2"))
+    if next_mod is not None:
+        n = next_mod.float().unsqueeze(1).chunk(12, dim=-1)
+        img, hi = k.gated_add_mod(img, i_g2, oi, n[0], n[1], dt, guard)
+        txt, ht = k.gated_add_mod(txt, t_g2, ot, n[6], n[7], dt, guard)
+        return img, txt, (hi, ht)
     img = k.gated_add(img, i_g2, oi, guard)
     txt = k.gated_add(txt, t_g2, ot, guard)
     return img, txt
 
 
-def single_block(w, x, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kernels = FUSED):
-    """x [B, Lt+Li, D] fp32, mod [B, 3D]."""
+def single_block(w, x, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kernels = FUSED, h=None,
+                 next_mod=None):
+    """x [B, Lt+Li, D] fp32, mod [B, 3D].
+
+    ``h``: linear1's input, mod_in(x) with this block's shift and scale, when the previous block computed
+    it. With ``next_mod`` (the next single block's [B, 3D]) the closing residual add also computes the next
+    block's ``h`` in the same pass (gated_add_mod) and the result is ``(x, h_next)``."""
     sh, sc, g = mod.float().unsqueeze(1).chunk(3, dim=-1)
     f32 = torch.float32
+    if h is None:
+        h = k.mod_in(x, sh, sc, dt)
+
+    def close(out):
+        if next_mod is None:
+            return k.gated_add(x, g, out, guard)
+        nsh, nsc, _ = next_mod.float().unsqueeze(1).chunk(3, dim=-1)
+        return k.gated_add_mod(x, g, out, nsh, nsc, dt, guard)
+
     if _fused_gelu(w, k):
         # linear1 writes its MLP columns, GELU'd, straight into linear2's input [attention | GELU(mlp)] and
         # the attention its output into the first columns: the bits of k.attn_mlp without its round trip.
         b, l, d = x.shape
         cat = torch.empty(b, l, d + cfg.mlp_hidden, dtype=dt, device=x.device)
-        ((qkv, _),) = w.linear_gelu_many([(k.mod_in(x, sh, sc, dt), "linear1", cfg.mlp_hidden, cat[..., d:])])
+        ((qkv, _),) = w.linear_gelu_many([(h, "linear1", cfg.mlp_hidden, cat[..., d:])])
+        del h
         q, kk, v = k.qkv_single(qkv, w.get("norm.query_norm.scale", f32), w.get("norm.key_norm.scale", f32), cos,
                                 sin, cfg.heads, dt)
         del qkv
@@ -162,8 +195,8 @@ def single_block(w, x, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kerne
         del q, kk, v
         out = w.linear(cat, "linear2")
         del cat
-        return k.gated_add(x, g, out, guard)
-    h = w.linear(k.mod_in(x, sh, sc, dt), "linear1")
+        return close(out)
+    h = w.linear(h, "linear1")
     qkv, mlp = h.split([3 * cfg.hidden, cfg.mlp_hidden], dim=-1)
     q, kk, v = k.qkv_single(qkv, w.get("norm.query_norm.scale", f32), w.get("norm.key_norm.scale", f32), cos, sin,
                             cfg.heads, dt)
@@ -171,7 +204,7 @@ def single_block(w, x, mod, cos, sin, cfg: FluxConfig, dt, guard: bool, k: Kerne
     del q, kk, v, qkv
     out = w.linear(k.attn_mlp(a, mlp), "linear2")
     del h, mlp, a
-    return k.gated_add(x, g, out, guard)
+    return close(out)
 
 
 def final_layer(w, img, fmod, dt, k: Kernels = FUSED):
@@ -334,13 +367,22 @@ class RandomFlux:
         cfg, dt, guard = self.cfg, self.dt, self.dt == torch.float16
         img = self.globals.linear(latents.to(dt), "img_in").float()
         lt = txt.shape[1]
-        nd = len(self.doubles)
+        nd, ns = len(self.doubles), len(self.singles)
+        # Between blocks of one kind, the closing residual add and the next block's mod_in run as one
+        # pass (gated_add_mod); the bits are those of the two kernels (same fp32 residual, same statistics).
+        chain = CHAIN_BLOCKS and isinstance(k, Kernels)
+        h = None
         for i, w in enumerate(self.doubles):
-            img, txt = double_block(w, img, txt, mods_s[i], cos, sin, cfg, dt, guard, k)
+            nxt = mods_s[i + 1] if chain and i + 1 < nd else None
+            r = double_block(w, img, txt, mods_s[i], cos, sin, cfg, dt, guard, k, h, nxt)
+            img, txt, h = r if nxt is not None else (*r, None)
         x = torch.cat((txt, img), dim=1)
         del txt, img
+        h = None
         for j, w in enumerate(self.singles):
-            x = single_block(w, x, mods_s[nd + j], cos, sin, cfg, dt, guard, k)
+            nxt = mods_s[nd + j + 1] if chain and j + 1 < ns else None
+            r = single_block(w, x, mods_s[nd + j], cos, sin, cfg, dt, guard, k, h, nxt)
+            x, h = r if nxt is not None else (r, None)
         return final_layer(self.globals, x[:, lt:], final_mod_s, dt, k)
 
 

@@ -127,6 +127,26 @@ def test_batched_step_equals_images_one_by_one(model):
         assert rel(out[i:i + 1], one.cpu()) < 1e-3
 
 
+def test_chained_blocks_equal_separate_segments(model, monkeypatch):
+    # RandomFlux.step runs each block's closing residual add together with the next block's mod_in
+    # (gated_add_mod); the velocity must be bit for bit that of the separate gated_add + mod_in kernels.
+    dev = torch.device("cuda")
+    g = seeded(30)
+    mods = model.modulations(torch.nn.functional.silu(torch.randn(3, 2, CFG.hidden, generator=g))
+                             .to(torch.bfloat16).to(dev))
+    _, txt, cos, sin = inputs(2, 64, 8)
+    lat = torch.randn(2, 64, 64, generator=g)
+    fmod = (torch.randn(2, 2 * CFG.hidden, generator=g) * 0.3).to(torch.bfloat16)
+
+    def run():
+        return model.step(lat.to(dev), txt.to(dev), [m[1] for m in mods], fmod.to(dev), cos.to(dev), sin.to(dev))
+
+    chained = run()
+    monkeypatch.setattr(F, "CHAIN_BLOCKS", False)
+    separate = run()
+    assert torch.isfinite(chained).all() and torch.equal(chained, separate)
+
+
 def test_fused_gelu_blocks_equal_composed_blocks(model, monkeypatch):
     # linear1 / mlp.0 with GELU in the GEMM epilogue, written into linear2's input next to the attention
     # output, against the unfused sequence (linear, GELU kernel, attention, concat): bit for bit.

@@ -287,7 +287,9 @@ __global__ __launch_bounds__(kI8GemvThreads, 4) void int8_row_gemv_kernel(
 //
 // For M <= 32 and K = 1024, 2048, 3072 (the hoisted modulation linears have
 // K = hidden = 3072). One workgroup of NW waves per CU streams 32-row slabs
-// ("units") of one or many weights.
+// ("units") of one or many weights; the units are dealt out round-robin
+// (workgroup b takes units b, b + G, b + 2G, ... for a grid of G), so that at
+// any time the CUs read one contiguous window of the weights.
 //
 //   * Wave w owns the K slice of blocks [w*BPW, (w+1)*BPW) (K = 64*NW*BPW) and
 //     keeps x for that slice in registers for the whole launch, as fp16 MFMA
@@ -297,8 +299,9 @@ __global__ __launch_bounds__(kI8GemvThreads, 4) void int8_row_gemv_kernel(
 //     scales (32 rows x K/64 floats, one contiguous block) are copied by the
 //     waves together into a shared double buffer. Consecutive lanes fetch
 //     consecutive 16-byte chunks, so every request covers whole cache lines;
-//     the chunk order inside a code row is XOR-swizzled so that the MFMA-order
-//     reads (lane (c, h) reads row c) are free of bank conflicts.
+//     the chunk order inside a code row, and inside a row of scales, is
+//     XOR-swizzled so that the MFMA-order reads (lane (c, h) reads row c) are
+//     free of bank conflicts.
 //   * Once its codes are in registers a wave issues the next unit's DMA and
 //     multiplies: each code byte is looked up in a 64-way replicated LDS table
 //     of fp16 code pairs (one v_perm for the address, one ds_read_b32), four
@@ -457,6 +460,7 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   uint8_t *stage = lds + L::kStage + wave * L::kCodeBytes;
   // MFMA-order reads: lane (c, h) takes chunk 2b + h of row c.
   const int rd_base = c * L::kChunks * 16, rd_swz = sg_swz<L::kChunks>(c);
+  const int sc_swz = sg_swz<kblocks / 4>(c);
   // v_perm source for table addresses: byte 0 = 4 * lane, byte 1 <- code byte.
   const uint32_t tsel = static_cast<uint32_t>(lane) * 4u;
 
@@ -500,9 +504,11 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   }
 
   const int units_total = prefix[count];
-  const int units_per_wg = (units_total + gridDim.x - 1) / gridDim.x;
-  const int u_begin = blockIdx.x * units_per_wg;
-  const int u_end = min(u_begin + units_per_wg, units_total);
+  // Units are dealt out round-robin: workgroup b takes units b, b + G, b + 2G, ... (G = grid size), so
+  // that at any time the CUs stream one contiguous window of the weights.
+  const int G = gridDim.x;
+  const int u_begin = blockIdx.x;
+  const int u_end = units_total;
   if (u_begin >= u_end) return;  // uniform over the workgroup
 
   auto locate = [&](int u, int g) {
@@ -511,12 +517,13 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   };
   // Descriptors are uniform: kept in scalar registers and reloaded only when the weight changes.
   auto desc = [&](int g) { return uniform_desc(descs ? descs[g] : one); };
-  auto scales = [&](int u) { return reinterpret_cast<float *>(lds + L::kScales + ((u - u_begin) & 1) * L::kScaleBytes); };
+  // Scale buffer of the workgroup's it-th unit (double buffered).
+  auto scales = [&](int it) { return reinterpret_cast<float *>(lds + L::kScales + (it & 1) * L::kScaleBytes); };
   // Code instruction j fetches chunk (p ^ swz(r)) of row r into stage slot
   // 64j + lane = r*kChunks + p; scale instructions j = wave, wave + NW, ... fetch
   // 1 KiB each. The buffers start at the unit's first row, so rows past the
   // weight's end fall outside their ranges and read as 0.
-  auto issue = [&](int u, const SDesc &d, int row0) {
+  auto issue = [&](int it, const SDesc &d, int row0) {
     const auto rc = make_rsrc(d.packed + static_cast<int64_t>(row0) * row_bytes,
                               static_cast<uint32_t>(max(d.n - row0, 0)) * row_bytes);
 #pragma unroll
@@ -529,8 +536,13 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
 #pragma unroll
     for (int jj = 0; jj < (L::kScaleInstrs + NW - 1) / NW; ++jj) {
       const int j = wave + NW * jj;
-      if (j < L::kScaleInstrs)
-        load_lds16_at(ra, reinterpret_cast<uint8_t *>(scales(u)) + 1024 * j, 1024 * j + 16 * lane);
+      if (j < L::kScaleInstrs) {
+        // slot s holds chunk (q ^ swz(r)) of row r, so that the 32 rows' reads of one scale spread over
+        // the banks (row r's scales at a fixed stride alone would share 4 banks)
+        const uint32_t s = 64u * j + lane, r = s / (kblocks / 4), q = s - r * (kblocks / 4);
+        load_lds16_at(ra, reinterpret_cast<uint8_t *>(scales(it)) + 1024 * j,
+                      (r * (kblocks / 4) + (q ^ sg_swz<kblocks / 4>(r))) * 16u);
+      }
     }
   };
   // Bias and outputs go through buffer resources, not generic pointers: a
@@ -573,13 +585,16 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   // This wave's codes and scales of unit u, from LDS into registers.
   uint4 cw[BPW];
   float a[BPW];
-  auto read_stage = [&](int u) {
-    const float *sc = scales(u) + c * kblocks + kb0;
+  auto read_stage = [&](int it) {
+    const float *sc = scales(it) + c * kblocks;
 #pragma unroll
     for (int b = 0; b < BPW; ++b)
       cw[b] = *reinterpret_cast<const uint4 *>(stage + rd_base + 16 * ((2 * b + h) ^ rd_swz));
 #pragma unroll
-    for (int b = 0; b < BPW; ++b) a[b] = sc[b];
+    for (int b = 0; b < BPW; ++b) {
+      const int f = kb0 + b;
+      a[b] = sc[4 * ((f >> 2) ^ sc_swz) + (f & 3)];
+    }
   };
 
   // Unit u of the loop: weight g_cur (descriptor d_cur, first row row_cur); the
@@ -587,27 +602,28 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   int g_cur = locate(u_begin, 0);
   SDesc d_cur = desc(g_cur);
   int row_cur = (u_begin - prefix[g_cur]) * kSgRows;
-  issue(u_begin, d_cur, row_cur);
+  issue(0, d_cur, row_cur);
   wait_vmcnt<0>();
   __syncthreads();  // the first unit's codes and scales are in LDS
-  read_stage(u_begin);
+  read_stage(0);
   SDesc d_prev = d_cur;
   int row_prev = row_cur;
   uint32_t bias_prev = 0;
-  for (int u = u_begin; u < u_end; ++u) {
-    const int buf = (u - u_begin) & (L::kRedBufs - 1);
+  int it = 0;
+  for (int u = u_begin; u < u_end; u += G, ++it) {
+    const int buf = it & (L::kRedBufs - 1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage read before the next DMA overwrites it
     const uint32_t bias_cur = load_bias(d_cur, row_cur);
-    int g_nxt = g_cur, row_nxt = row_cur + kSgRows;
+    int g_nxt = g_cur, row_nxt = row_cur;
     SDesc d_nxt = d_cur;
-    const bool more = u + 1 < u_end;
-    if (more && row_nxt >= d_cur.n) {
-      g_nxt = locate(u + 1, g_cur);
-      d_nxt = desc(g_nxt);
-      row_nxt = (u + 1 - prefix[g_nxt]) * kSgRows;
+    const bool more = u + G < u_end;
+    if (more) {
+      g_nxt = locate(u + G, g_cur);
+      if (g_nxt != g_cur) d_nxt = desc(g_nxt);
+      row_nxt = (u + G - prefix[g_nxt]) * kSgRows;
     }
     if (u > u_begin) finish(buf ^ (L::kRedBufs - 1), d_prev, row_prev, bias_prev);  // unit u-1
-    if (more) issue(u + 1, d_nxt, row_nxt);
+    if (more) issue(it + 1, d_nxt, row_nxt);
 
     // Table lookups run kSgAhead sub-steps ahead of the MFMAs that use them.
     auto word = [&](int t) {
@@ -655,13 +671,13 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
       __syncthreads();  // every wave has summed unit u-1 from the single buffer
 #pragma unroll
       for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r];
-      if (more) read_stage(u + 1);  // its latency overlaps the barrier
+      if (more) read_stage(it + 1);  // its latency overlaps the barrier
       __syncthreads();
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r];
       __syncthreads();  // partials of unit u complete; every wave's DMAs of unit u+1 landed
-      if (more) read_stage(u + 1);
+      if (more) read_stage(it + 1);
     }
     d_prev = d_cur;
     row_prev = row_cur;
@@ -670,7 +686,7 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     d_cur = d_nxt;
     row_cur = row_nxt;
   }
-  finish((u_end - 1 - u_begin) & (L::kRedBufs - 1), d_prev, row_prev, bias_prev);
+  finish((it - 1) & (L::kRedBufs - 1), d_prev, row_prev, bias_prev);
 }
 
 // ------------------------------------------------------- int8_row streaming skinny GEMM

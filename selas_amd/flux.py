@@ -100,6 +100,15 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
 CHAIN_BLOCKS = True
 
 
+def _fp32_vectors(vs: list[torch.Tensor]) -> list[torch.Tensor]:
+    """[B, n_i] vectors as fp32 views of one converted [B, sum n_i] tensor (a copy and one conversion
+    for all of them); vectors already fp32 are returned as they are."""
+    if all(v.dtype == torch.float32 for v in vs):
+        return vs
+    flat = torch.cat([v.reshape(v.shape[0], -1) for v in vs], dim=-1).float()
+    return list(flat.split([v.shape[-1] for v in vs], dim=-1))
+
+
 def _fused_gelu(w, k) -> bool:
     """The GELU after the MLP input linears goes into the GEMM epilogue when the unit can do that and the
     segments are this package's kernels (whose GELU the epilogue reproduces bit for bit)."""
@@ -365,6 +374,9 @@ class RandomFlux:
         """Velocity for one step (flux.py:527-582). latents [B, Li, 64] fp32, txt [B, Lt, D] fp32,
         mods_s: per block [B, kD] for this step, final_mod_s [B, 2D]."""
         cfg, dt, guard = self.cfg, self.dt, self.dt == torch.float16
+        # The blocks use their modulation vectors in fp32 (each block converts its own, flux.py:302, 327):
+        # one conversion of all of them is exact and saves a small kernel per block.
+        *mods_s, final_mod_s = _fp32_vectors([*mods_s, final_mod_s])
         img = self.globals.linear(latents.to(dt), "img_in").float()
         lt = txt.shape[1]
         nd, ns = len(self.doubles), len(self.singles)

@@ -1026,6 +1026,12 @@ __device__ __forceinline__ bf16x8 dequant8(const Tables &t, uint32_t P) {
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 
+// A compile-time bool for generic lambdas (decltype(tag)::value).
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 // Interleaving of one sub-step: after each of the N MFMAs, V VALU
 // instructions, and one LDS read after every R-th MFMA.
 template <int N, int R, int V>
@@ -1360,16 +1366,6 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
 
   // Epilogue: acc[mb][cb] holds D[n][m] for n = n0 + WN*wave + 32*cb + 8*(r/4) + 4*h + r%4
   // and m = m0 + 32*mb + c. Bias is added in fp32 and the sum rounded once.
-  float bv[CB][4][4];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int t4 = 0; t4 < 4; ++t4) {
-        const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h + t4;
-        bv[cb][q][t4] = (bias && n < N) ? bf16_bits_to_f32(bias[n]) : 0.0f;
-      }
   // A tile past n_split holds GELU columns (uniform over the workgroup): the sum
   // is rounded to bf16 as it would be stored, GELU'd in fp32 and rounded again,
   // exactly what a separate GELU kernel reading the stored output computes.
@@ -1381,10 +1377,25 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
     const __bf16 r = static_cast<__bf16>(materialize(v));
     return bf16_bits_rne(gelu_tanh_fast(static_cast<float>(r)));
   };
-  auto out2 = [&](float a, float b) -> uint32_t {
-    if (gelu) return gelu1(a) | (static_cast<uint32_t>(gelu1(b)) << 16);
-    return pack_bf16x2(a, b);
-  };
+  // The output goes through LDS when the wave's 64 columns lie inside N and the
+  // output rows are 16-byte aligned (every full tile of the block linears).
+  const bool staged = n0 + WN * (wave + 1) <= N && (ldo & 7) == 0 && (reinterpret_cast<uintptr_t>(Yo) & 15) == 0;
+  // The staged path's bias: 2-byte buffer loads with no branches, all issued
+  // before the drain below so that their latency overlaps it (a null bias is an
+  // empty range and reads as zeros). Per-element guarded loads, each waited
+  // for in turn, took ~1.5 us per tile.
+  uint32_t bb[CB][4][4];
+  if (staged) {
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(bias, bias ? static_cast<uint32_t>(N) * 2u : 0u);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4)
+          bb[cb][q][t4] = __builtin_amdgcn_raw_buffer_load_b16(
+              br, static_cast<uint32_t>(n0 + WN * wave + 32 * cb + 8 * q + 4 * h + t4) * 2u, 0, 0);
+  }
   // Every wave is done with the x stages before any wave stages its output
   // there: its own loads into LDS have landed (the last K blocks' look-ahead
   // DMAs may still be in flight; the workgroup barrier alone does not wait for
@@ -1393,50 +1404,80 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // it, and it also leaves no DMA in flight when the workgroup ends.
   wait_vmcnt<0>();
   __syncthreads();
-  const bool full_cols = n0 + WN * (wave + 1) <= N;
-  if (full_cols && (ldo & 7) == 0 && (reinterpret_cast<uintptr_t>(Yo) & 15) == 0) {
+  if (staged) {
     // Through LDS, so that every store writes whole 128-byte row segments: a
     // direct store from the MFMA layout writes 16 bytes into each of 32 rows,
     // and each partial line then reaches HBM as a write of its own. Each wave
     // stages HR*32 rows x WN columns at a time (row stride WN*2+8 bytes: the
     // 8-byte writes of 32 lanes then hit distinct banks), in its own region.
+    // The GELU choice is made once for the whole tile: tested per value pair,
+    // its branches took ~3 us per tile of the 256-row kernel.
     constexpr int RS = WN * 2 + 8;
     constexpr int HR = (MB % 2 == 0 && NW * (MB / 2) * 32 * RS <= STAGES * SB) ? MB / 2 : 1;
     static_assert(NW * HR * 32 * RS <= STAGES * SB && MB % HR == 0, "epilogue staging fits the x stages");
     uint8_t *ep = smem + wave * HR * 32 * RS;
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(Yo, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldo * 2,
                                                                               static_cast<int64_t>(0xffffffff))));
+    auto stage_out = [&](auto gelu_tag) {
+      constexpr bool G = decltype(gelu_tag)::value;
 #pragma unroll
-    for (int piece = 0; piece < MB / HR; ++piece) {
+      for (int piece = 0; piece < MB / HR; ++piece) {
 #pragma unroll
-      for (int mh = 0; mh < HR; ++mh) {
-        const int mb = HR * piece + mh;
+        for (int mh = 0; mh < HR; ++mh) {
+          const int mb = HR * piece + mh;
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
+          for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = out2(acc[mb][cb][4 * q] + bv[cb][q][0], acc[mb][cb][4 * q + 1] + bv[cb][q][1]);
-            const uint32_t hi = out2(acc[mb][cb][4 * q + 2] + bv[cb][q][2], acc[mb][cb][4 * q + 3] + bv[cb][q][3]);
-            *reinterpret_cast<uint2 *>(ep + (32 * mh + c) * RS + 2 * (32 * cb + 8 * q + 4 * h)) = make_uint2(lo, hi);
-          }
+            for (int q = 0; q < 4; ++q) {
+              float v[4];
+#pragma unroll
+              for (int t4 = 0; t4 < 4; ++t4) v[t4] = acc[mb][cb][4 * q + t4] + bf16_bits_to_f32(bb[cb][q][t4]);
+              uint32_t lo, hi;
+              if constexpr (G) {
+                lo = gelu1(v[0]) | (static_cast<uint32_t>(gelu1(v[1])) << 16);
+                hi = gelu1(v[2]) | (static_cast<uint32_t>(gelu1(v[3])) << 16);
+              } else {
+                lo = pack_bf16x2(v[0], v[1]);
+                hi = pack_bf16x2(v[2], v[3]);
+              }
+              *reinterpret_cast<uint2 *>(ep + (32 * mh + c) * RS + 2 * (32 * cb + 8 * q + 4 * h)) = make_uint2(lo, hi);
+            }
+        }
+        // Row r of the staged block: WN/8 lanes x 16 bytes; a wave stores 512/WN rows per instruction.
+        constexpr int LPR = WN / 8, RPI = 64 / LPR;
+#pragma unroll
+        for (int j = 0; j < HR * 32 / RPI; ++j) {
+          const int r = RPI * j + lane / LPR, col = 8 * (lane % LPR);
+          const uint8_t *src = ep + r * RS + 2 * col;
+          const uint2 v0 = *reinterpret_cast<const uint2 *>(src), v1 = *reinterpret_cast<const uint2 *>(src + 8);
+          const int m = m0 + 32 * HR * piece + r;
+          // Rows past M fall outside the buffer range and are dropped.
+          const uint32_t off = m < M ? static_cast<uint32_t>((static_cast<int64_t>(m) * ldo + n0 - cs + WN * wave + col) * 2)
+                                     : 0xffffffffu;
+          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{v0.x, v0.y, v1.x, v1.y}, yr, off, 0, 0);
+        }
       }
-      // Row r of the staged block: WN/8 lanes x 16 bytes; a wave stores 512/WN rows per instruction.
-      constexpr int LPR = WN / 8, RPI = 64 / LPR;
-#pragma unroll
-      for (int j = 0; j < HR * 32 / RPI; ++j) {
-        const int r = RPI * j + lane / LPR, col = 8 * (lane % LPR);
-        const uint8_t *src = ep + r * RS + 2 * col;
-        const uint2 v0 = *reinterpret_cast<const uint2 *>(src), v1 = *reinterpret_cast<const uint2 *>(src + 8);
-        const int m = m0 + 32 * HR * piece + r;
-        // Rows past M fall outside the buffer range and are dropped.
-        const uint32_t off =
-            m < M ? static_cast<uint32_t>((static_cast<int64_t>(m) * ldo + n0 - cs + WN * wave + col) * 2) : 0xffffffffu;
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v0.x, v0.y, v1.x, v1.y}, yr, off, 0, 0);
-      }
-    }
+    };
+    if (gelu) stage_out(BoolTag<true>{});
+    else stage_out(BoolTag<false>{});
     return;
   }
+  // Direct stores (partial column tiles, unaligned outputs).
+  float bv[CB][4][4];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const int n = n0 + WN * wave + 32 * cb + 8 * q + 4 * h + t4;
+        bv[cb][q][t4] = (bias && n < N) ? bf16_bits_to_f32(bias[n]) : 0.0f;
+      }
+  auto out2 = [&](float a, float b) -> uint32_t {
+    if (gelu) return gelu1(a) | (static_cast<uint32_t>(gelu1(b)) << 16);
+    return pack_bf16x2(a, b);
+  };
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll

@@ -1131,7 +1131,8 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   constexpr int XL = 4 * MB / NW;   // x DMAs (8 rows each) per K block and wave
   constexpr int LPB = 2 * CB + XL;  // vector-memory loads issued per K block and wave
   static_assert(MB * CB * NW <= 64 && 4 * MB % NW == 0 && (STAGES == 2 || STAGES == 3), "tile shape");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB];
+  // The x stages, then 1 KiB per wave for its bias columns.
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB + NW * 1024];
   const int t = (blockIdx.x & 7) * batch.per_xcd + (blockIdx.x >> 3);
   if (t >= batch.tiles) return;
   // The problem this tile belongs to (uniform: scalar selects over the kernel arguments).
@@ -1272,6 +1273,15 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // Every iteration issues the loads of block kb+LOOK; past the last block the
   // last block is loaded again (valid addresses, into the stage that is free)
   // so that the loop body has no branches and schedules as one region.
+  // The wave's 64 bias values (128 bytes) into its LDS bias area by DMA, ahead of
+  // the first block's loads (the first wait below covers it); the staged
+  // epilogue reads them there instead of waiting for loads issued after the K
+  // loop. Lanes 8-63 read past the range and write zeros.
+  uint8_t *const bias_lds = smem + STAGES * SB + wave * 1024;
+  const bool bias_dma = bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 15) == 0;
+  if (bias_dma)
+    load_lds16(make_rsrc(bias, static_cast<uint32_t>(N) * 2u), bias_lds,
+               lane < 8 ? static_cast<uint32_t>(n0 + WN * wave + 8 * lane) * 2u : 0xfffffff0u, 0);
   WR w0, w1, w2;
   issue(0, 0, w0);
   if constexpr (STAGES == 3) {
@@ -1380,12 +1390,13 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // The output goes through LDS when the wave's 64 columns lie inside N and the
   // output rows are 16-byte aligned (every full tile of the block linears).
   const bool staged = n0 + WN * (wave + 1) <= N && (ldo & 7) == 0 && (reinterpret_cast<uintptr_t>(Yo) & 15) == 0;
-  // The staged path's bias: 2-byte buffer loads with no branches, all issued
+  // The staged path's bias: from the wave's LDS bias area when the prologue
+  // loaded it there, else 2-byte buffer loads with no branches, all issued
   // before the drain below so that their latency overlaps it (a null bias is an
   // empty range and reads as zeros). Per-element guarded loads, each waited
-  // for in turn, took ~1.5 us per tile.
+  // for in turn, took ~1.5 us per tile; loads issued after the K loop, ~1 us.
   uint32_t bb[CB][4][4];
-  if (staged) {
+  if (staged && !bias_dma) {
     const __amdgpu_buffer_rsrc_t br = make_rsrc(bias, bias ? static_cast<uint32_t>(N) * 2u : 0u);
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
@@ -1405,6 +1416,18 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   wait_vmcnt<0>();
   __syncthreads();
   if (staged) {
+    if (bias_dma) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint2 v = *reinterpret_cast<const uint2 *>(bias_lds + 2 * (32 * cb + 8 * q + 4 * h));
+          bb[cb][q][0] = v.x & 0xffffu;
+          bb[cb][q][1] = v.x >> 16;
+          bb[cb][q][2] = v.y & 0xffffu;
+          bb[cb][q][3] = v.y >> 16;
+        }
+    }
     // Through LDS, so that every store writes whole 128-byte row segments: a
     // direct store from the MFMA layout writes 16 bytes into each of 32 rows,
     // and each partial line then reaches HBM as a write of its own. Each wave
@@ -1418,6 +1441,13 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
     uint8_t *ep = smem + wave * HR * 32 * RS;
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(Yo, static_cast<uint32_t>(min(static_cast<int64_t>(M) * ldo * 2,
                                                                               static_cast<int64_t>(0xffffffff))));
+    // The lane index again, opaque to the compiler: values derived from it here
+    // are then not shared with the prologue's, which the register-bound K loop
+    // would spill (a reload before every store, each waiting for the stores
+    // issued before it).
+    int lo_lane = tid & 63;
+    asm volatile("" : "+v"(lo_lane));
+    const int ec = lo_lane & 31, eh = lo_lane >> 5;
     auto stage_out = [&](auto gelu_tag) {
       constexpr bool G = decltype(gelu_tag)::value;
 #pragma unroll
@@ -1440,14 +1470,14 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
                 lo = pack_bf16x2(v[0], v[1]);
                 hi = pack_bf16x2(v[2], v[3]);
               }
-              *reinterpret_cast<uint2 *>(ep + (32 * mh + c) * RS + 2 * (32 * cb + 8 * q + 4 * h)) = make_uint2(lo, hi);
+              *reinterpret_cast<uint2 *>(ep + (32 * mh + ec) * RS + 2 * (32 * cb + 8 * q + 4 * eh)) = make_uint2(lo, hi);
             }
         }
         // Row r of the staged block: WN/8 lanes x 16 bytes; a wave stores 512/WN rows per instruction.
         constexpr int LPR = WN / 8, RPI = 64 / LPR;
 #pragma unroll
         for (int j = 0; j < HR * 32 / RPI; ++j) {
-          const int r = RPI * j + lane / LPR, col = 8 * (lane % LPR);
+          const int r = RPI * j + lo_lane / LPR, col = 8 * (lo_lane % LPR);
           const uint8_t *src = ep + r * RS + 2 * col;
           const uint2 v0 = *reinterpret_cast<const uint2 *>(src), v1 = *reinterpret_cast<const uint2 *>(src + 8);
           const int m = m0 + 32 * HR * piece + r;

@@ -1270,9 +1270,6 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[mb][cb] = f32x16{};
 
-  // Every iteration issues the loads of block kb+LOOK; past the last block the
-  // last block is loaded again (valid addresses, into the stage that is free)
-  // so that the loop body has no branches and schedules as one region.
   // The wave's 64 bias values (128 bytes) into its LDS bias area by DMA, ahead of
   // the first block's loads (the first wait below covers it); the staged
   // epilogue reads them there instead of waiting for loads issued after the K
@@ -1282,6 +1279,9 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   if (bias_dma)
     load_lds16(make_rsrc(bias, static_cast<uint32_t>(N) * 2u), bias_lds,
                lane < 8 ? static_cast<uint32_t>(n0 + WN * wave + 8 * lane) * 2u : 0xfffffff0u, 0);
+  // Every iteration issues the loads of block kb+LOOK; past the last block the
+  // last block is loaded again (valid addresses, into the stage that is free)
+  // so that the loop body has no branches and schedules as one region.
   WR w0, w1, w2;
   issue(0, 0, w0);
   if constexpr (STAGES == 3) {

@@ -244,6 +244,28 @@ def test_tile_height_does_not_change_the_bits(dev):
     check_close(small, oracle_linear(x[:300], w_ref, b))
 
 
+@pytest.mark.parametrize("n", [1024, 1000])
+def test_bias_alignment_does_not_change_the_bits(dev, n):
+    # The tiled kernel brings a 16-byte aligned bias into LDS by DMA and reads any other bias
+    # with 2-byte loads; a bias view at a 2-byte offset must give the same bits as an aligned
+    # copy. N = 1000 leaves the last column tile partial (per-element bias there).
+    k = 256
+    p, a, w_ref = make_weight(n, k, 71, dev)
+    x = torch.randn(600, k, generator=seeded(72)).to(torch.bfloat16).to(dev)
+    buf = (torch.randn(n + 8, generator=seeded(73)) * 0.02).to(torch.bfloat16).to(dev)
+    b_odd = buf[1:n + 1]
+    assert b_odd.data_ptr() % 16 != 0
+    b_al = b_odd.clone()
+    assert b_al.data_ptr() % 16 == 0
+    y_odd = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b_odd)
+    y_al = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b_al)
+    assert torch.equal(y_odd, y_al)
+    check_close(y_al, oracle_linear(x, w_ref, b_al))
+    # no bias: the kernel reads an empty range (zeros)
+    y_none = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None)
+    check_close(y_none, oracle_linear(x, w_ref, None))
+
+
 def test_224_row_tiles_give_the_same_bits(dev):
     # On a 256-CU GPU, M = 448, N = 44032 (172 column tiles) runs 224-row tiles: 344 tiles in two
     # rounds, where 192-row tiles would need three; its 2048-row superset runs 256-row tiles. The

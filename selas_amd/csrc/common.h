@@ -75,15 +75,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // GELU with the tanh approximation, x * 0.5 * (1 + tanh(z)), z = sqrt(2/pi) *
-// (x + 0.044715 x^3), through 0.5 * (1 + tanh(z)) = 1 / (1 + exp(-2z)): one
-// hardware exponential and one reciprocal instead of tanhf (a few ulp of fp32,
+// (x + 0.044715 x^3), through 0.5 * (1 + tanh(z)) = 1 / (1 + exp(-2z)) =
+// 1 / (1 + 2^u), u = x (A + B x^2), A = -2 log2(e) sqrt(2/pi), B = 0.044715 A:
+// one multiply, one fused multiply-add, one multiply, then one hardware
+// base-2 exponential and one reciprocal instead of tanhf (a few ulp of fp32,
 // below the rounding to a 16-bit output). One definition serves the segment
 // kernels and the GEMM epilogue, so both give the same bits.
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
-  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
-  const float kKappa = 0.044715f;
-  const float z = kBeta * (x + kKappa * x * x * x);
-  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * z));
+  constexpr float kA = -2.302208198144325f;   // -2 log2(e) sqrt(2 / pi)
+  constexpr float kB = -0.1029432395800235f;  // 0.044715 kA
+  const float u = x * __builtin_fmaf(kB, x * x, kA);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u));
 }
 
 // fp32 -> bf16 bits, round to nearest even (the rounding torch uses for
@@ -138,6 +140,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   bf16x2 v = {static_cast<__bf16>(materialize(lo)), static_cast<__bf16>(materialize(hi))};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// GELU of two values rounded as a packed bf16 pair (the hardware convert).
+__device__ __forceinline__ uint32_t gelu_bf16x2(float lo, float hi) {
+  return pack_bf16x2(gelu_tanh_fast(lo), gelu_tanh_fast(hi));
 }
 
 // Wave-wide (64 lanes) reductions through the cross-lane network.

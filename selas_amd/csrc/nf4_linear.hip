@@ -1383,9 +1383,10 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   uint16_t *const Yo = gelu ? P.Y2 : Y;
   const int64_t ldo = gelu ? P.ldy2 : ldy;
   const int cs = gelu ? P.n_split : 0;  // column shift into Yo
+  // GELU of the value rounded to bf16 as it would be stored (both roundings by the hardware convert).
   auto gelu1 = [](float v) {
-    const __bf16 r = static_cast<__bf16>(materialize(v));
-    return bf16_bits_rne(gelu_tanh_fast(static_cast<float>(r)));
+    const uint32_t r = pack_bf16x2(v, 0.0f);
+    return static_cast<uint16_t>(gelu_bf16x2(bf16_bits_to_f32(r & 0xffffu), 0.0f) & 0xffffu);
   };
   // The output goes through LDS when the wave's 64 columns lie inside N and the
   // output rows are 16-byte aligned (every full tile of the block linears).
@@ -1464,8 +1465,9 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
               for (int t4 = 0; t4 < 4; ++t4) v[t4] = acc[mb][cb][4 * q + t4] + bf16_bits_to_f32(bb[cb][q][t4]);
               uint32_t lo, hi;
               if constexpr (G) {
-                lo = gelu1(v[0]) | (static_cast<uint32_t>(gelu1(v[1])) << 16);
-                hi = gelu1(v[2]) | (static_cast<uint32_t>(gelu1(v[3])) << 16);
+                const uint32_t r01 = pack_bf16x2(v[0], v[1]), r23 = pack_bf16x2(v[2], v[3]);
+                lo = gelu_bf16x2(bf16_bits_to_f32(r01 & 0xffffu), bf16_bits_to_f32(r01 >> 16));
+                hi = gelu_bf16x2(bf16_bits_to_f32(r23 & 0xffffu), bf16_bits_to_f32(r23 >> 16));
               } else {
                 lo = pack_bf16x2(v[0], v[1]);
                 hi = pack_bf16x2(v[2], v[3]);

@@ -345,14 +345,16 @@ __global__ __launch_bounds__(256) void concat_gelu_kernel(const uint16_t *__rest
           float lo, hi;
           if constexpr (DT == SELAS_BF16) { lo = bf16_bits_to_f32(w[t] & 0xffffu); hi = bf16_bits_to_f32(w[t] >> 16); }
           else { lo = f16_bits_to_f32(w[t] & 0xffffu); hi = f16_bits_to_f32(w[t] >> 16); }
-          o[t] = pack_pair<DT>(gelu_tanh_fast(lo), gelu_tanh_fast(hi));
+          if constexpr (DT == SELAS_BF16) o[t] = gelu_bf16x2(lo, hi);
+          else o[t] = pack_pair<DT>(gelu_tanh_fast(lo), gelu_tanh_fast(hi));
         }
         *reinterpret_cast<uint4 *>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
       } else {
         float xv;
         if constexpr (DT == SELAS_BF16) xv = bf16_bits_to_f32(*src);
         else xv = f16_bits_to_f32(*src);
-        *dst = DT == SELAS_BF16 ? bf16_bits_rne(gelu_tanh_fast(xv)) : f16_bits_rne(gelu_tanh_fast(xv));
+        if constexpr (DT == SELAS_BF16) *dst = static_cast<uint16_t>(gelu_bf16x2(xv, 0.0f) & 0xffffu);
+        else *dst = f16_bits_rne(gelu_tanh_fast(xv));
       }
     }
   }

@@ -8,7 +8,11 @@
  *   - launches asynchronously on the HIP stream passed as `stream` (a
  *     hipStream_t; pass the caller's current stream so that stream-ordered
  *     buffer reuse stays correct) and never synchronises the device;
- *   - allocates nothing and frees nothing: outputs are caller-owned;
+ *   - allocates nothing and frees nothing: outputs are caller-owned (one
+ *     exception: the tiled NF4 linears allocate one 64 MiB workspace per
+ *     device and stream at their first launch that splits its last round of
+ *     tiles over K, and keep it until the process ends; a first call outside
+ *     HIP graph capture sets it up);
  *   - returns SELAS_OK or an error code and never throws; the message of the
  *     last error on the calling thread is returned by selas_last_error().
  *
@@ -19,8 +23,9 @@
  * (the tensor's meta["code"]); int8_row weights are `q` int8 in the weight's
  * shape and `scale` fp32, one per row.
  *
- * Kernels are chosen from shapes, dtypes and pointer alignment only and use
- * no atomics, so equal inputs give equal bits on every call.
+ * Kernels are chosen from shapes, dtypes and pointer alignment (and the GPU's
+ * CU count) only and use no atomics, so equal inputs give equal bits on every
+ * call.
  */
 #ifndef SELAS_AMD_H
 #define SELAS_AMD_H
@@ -105,7 +110,11 @@ int selas_int8_row_encode(const float *w, int64_t rows, int64_t cols, int8_t *q,
  * scales the fp32 block sums by absmax (for K = 1024, 2048, 3072 in fp16 after
  * an exact power-of-two rescale of each row of x; otherwise in bf16 with codes
  * split into two bf16 terms); it agrees with the decoded-weight product to the
- * rounding of the decoded weight. Returns SELAS_EUNSUPPORTED
+ * rounding of the decoded weight. Every output of the tiled GEMM sums K in
+ * one order, whatever M and the tile height, except where a launch splits its
+ * last round of tiles over K (long K and a last round of few tiles, e.g.
+ * M 6144, N 3072, K 15360): those tiles' K ranges are summed in fp32 by a
+ * second kernel, in a fixed order. Returns SELAS_EUNSUPPORTED
  * when the shape or layout is outside the fused kernels (blocksize != 64,
  * K % 64 != 0, misaligned rows, dtype other than bf16); the caller then
  * decodes with selas_nf4_dequant and uses a library GEMM.

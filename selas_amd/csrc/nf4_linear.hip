@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 
@@ -1116,12 +1117,47 @@ struct GemmProblem {
   int M, K, N, n_split, tiles_n, tile0;
 };
 constexpr int kGemmMaxProblems = 4;
+// Tiles [0, tiles - tail) run whole, one workgroup each: workgroup b < dp_blocks
+// takes tile (b % 8) * per_xcd + b / 8. The last `tail` tiles (a last round that
+// would leave most CUs idle) run as `split` K ranges each, one workgroup per
+// (range r, tile): item j = r * tail + q, taken by workgroup dp_blocks + b' with
+// j = (b' % 8) * tail_per_xcd + b' / 8, so each XCD runs one K range of
+// consecutive tiles. A split item leaves its fp32 partial tile in part[j] and
+// gemm_tail_sum adds the ranges in K order.
 struct GemmBatch {
   GemmProblem p[kGemmMaxProblems];
   int count, tiles, per_xcd;
+  int tail, split, dp_blocks, tail_per_xcd;
+  float *part;
 };
 
-template <WCodec WC, int MB, int CB, int STAGES, int NW>
+// Origin (m0, n0) of tile t of problem P (t in [P.tile0, P.tile0 + tiles)). The
+// tiles go in groups of kGroupM row slabs, the row index fastest inside a
+// group: the 32 tiles an XCD runs at once then cover 4 row slabs x 8 weight
+// strips instead of 1 x 32, so fewer distinct x and weight blocks miss its L2
+// per K step (linear1 558 us instead of 563 us).
+template <int TM, int TN>
+__device__ __forceinline__ void tile_origin(const GemmProblem &P, int t, int &m0, int &n0) {
+  constexpr int kGroupM = 4;
+  const int lt = t - P.tile0, tiles_m = (P.M + TM - 1) / TM, tiles_n = P.tiles_n;
+  const int group = lt / (kGroupM * tiles_n), first_m = group * kGroupM;
+  const int gm = min(kGroupM, tiles_m - first_m), in = lt - group * kGroupM * tiles_n;
+  m0 = (first_m + in % gm) * TM;
+  n0 = (in / gm) * TN;
+}
+
+// The problem a tile belongs to (uniform: scalar selects over the kernel arguments).
+__device__ __forceinline__ GemmProblem tile_problem(const GemmBatch &batch, int t) {
+  GemmProblem P = batch.p[0];
+#pragma unroll
+  for (int i = 1; i < kGemmMaxProblems; ++i)
+    if (i < batch.count && t >= batch.p[i].tile0) P = batch.p[i];
+  return P;
+}
+
+// SPLIT: the launch has split items (a kernel of its own, since the partial-tile
+// stores make the compiler spill registers in the epilogue of every tile).
+template <WCodec WC, int MB, int CB, int STAGES, int NW, bool SPLIT = false>
 __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) {
   constexpr bool kI8 = WC == WCodec::kInt8Row;
   using WR = WRegs<WC, CB>;
@@ -1133,44 +1169,51 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   static_assert(MB * CB * NW <= 64 && 4 * MB % NW == 0 && (STAGES == 2 || STAGES == 3), "tile shape");
   // The x stages, then 1 KiB per wave for its bias columns.
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * SB + NW * 1024];
-  const int t = (blockIdx.x & 7) * batch.per_xcd + (blockIdx.x >> 3);
-  if (t >= batch.tiles) return;
-  // The problem this tile belongs to (uniform: scalar selects over the kernel arguments).
-  GemmProblem P = batch.p[0];
-#pragma unroll
-  for (int i = 1; i < kGemmMaxProblems; ++i)
-    if (i < batch.count && t >= batch.p[i].tile0) P = batch.p[i];
-  const uint16_t *__restrict__ X = P.X;
-  const uint8_t *__restrict__ packed = P.packed;
-  const float *__restrict__ absmax = P.absmax;
+  // Work item: a whole tile t, or split item j (K range j / tail of tile t).
+  int t, j = -1;
+  if (!SPLIT || static_cast<int>(blockIdx.x) < batch.dp_blocks) {
+    t = (blockIdx.x & 7) * batch.per_xcd + (blockIdx.x >> 3);
+    if (t >= batch.tiles - (SPLIT ? batch.tail : 0)) return;
+  } else {
+    const int bt = static_cast<int>(blockIdx.x) - batch.dp_blocks;
+    j = (bt & 7) * batch.tail_per_xcd + (bt >> 3);
+    if (j >= batch.tail * batch.split) return;
+    t = batch.tiles - batch.tail + j % batch.tail;
+  }
+  const GemmProblem P = tile_problem(batch, t);
+  const int64_t ldx = P.ldx, ldy = P.ldy;
+  const int M = P.M, K = P.K, N = P.N;
+  const int kblocks = K >> 6;
+  // K blocks [kb_lo, kb_lo + nblk) of the tile: all of them, or range j / tail of `split` near-equal ranges.
+  int kb_lo = 0, nblk = kblocks;
+  if (SPLIT && j >= 0) {
+    const int r = j / batch.tail;
+    kb_lo = r * kblocks / batch.split;
+    nblk = (r + 1) * kblocks / batch.split - kb_lo;
+  }
+  // The operands start at block kb_lo; the loop below indexes blocks from 0.
+  const uint16_t *__restrict__ X = P.X + 64 * kb_lo;
+  const uint8_t *__restrict__ packed = P.packed + (kI8 ? 64 : 32) * kb_lo;
+  const float *__restrict__ absmax = P.absmax + (kI8 ? 0 : kb_lo);
   const uint16_t *__restrict__ bias = P.bias;
   uint16_t *__restrict__ Y = P.Y;
-  const int64_t ldx = P.ldx, ldy = P.ldy;
-  const int M = P.M, K = P.K, N = P.N, tiles_n = P.tiles_n;
   const int tid = threadIdx.x;
   // The wave index as a scalar: the LDS addresses of the x DMA (taken from M0) are then scalar arithmetic.
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, c = lane & 31;
-  // Tile order within the problem: groups of kGroupM row slabs, the row index
-  // fastest inside a group. The 32 tiles an XCD runs at once then cover 4 row
-  // slabs x 8 weight strips instead of 1 x 32, so fewer distinct x and weight
-  // blocks miss its L2 per K step (linear1 558 us instead of 563 us).
-  constexpr int kGroupM = 4;
-  const int lt = t - P.tile0, tiles_m = (M + TM - 1) / TM;
-  const int group = lt / (kGroupM * tiles_n), first_m = group * kGroupM;
-  const int gm = min(kGroupM, tiles_m - first_m), in = lt - group * kGroupM * tiles_n;
-  const int tm = first_m + in % gm, tn = in / gm;
-  const int m0 = tm * TM, n0 = tn * TN;
-  const int kblocks = K >> 6;
+  int m0, n0;
+  tile_origin<TM, TN>(P, t, m0, n0);
   const uint32_t ldx_b = static_cast<uint32_t>(ldx) * 2u;
 
   // Buffer resources; the range check covers the per-lane offset, which holds
-  // the row term, so rows past M or N read as zeros (never stored).
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(X, static_cast<uint32_t>(M) * ldx_b);
+  // the row term, so rows past M or N read as zeros (never stored). With the
+  // bases moved to block kb_lo the ranges shrink by the same amount, so the
+  // last row's blocks stay inside and the rows past the end stay outside.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(X, static_cast<uint32_t>(M) * ldx_b - 128u * kb_lo);
   const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(packed, static_cast<uint32_t>(N) * static_cast<uint32_t>(kI8 ? K : (K >> 1)));
+      make_rsrc(packed, static_cast<uint32_t>(N) * static_cast<uint32_t>(kI8 ? K : (K >> 1)) - (kI8 ? 64u : 32u) * kb_lo);
   const __amdgpu_buffer_rsrc_t sr =
-      make_rsrc(absmax, static_cast<uint32_t>(N) * static_cast<uint32_t>(kI8 ? 1 : kblocks) * 4u);
+      make_rsrc(absmax, static_cast<uint32_t>(N) * static_cast<uint32_t>(kI8 ? 1 : kblocks) * 4u - (kI8 ? 0u : 4u) * kb_lo);
 
   // x tile DMA: wave w fills tile rows [8*XL*w, 8*XL*(w+1)) with XL loads of 8
   // rows; lane i of load j lands at row r = 8*XL*w + 8j + i/8, physical
@@ -1275,7 +1318,7 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // epilogue reads them there instead of waiting for loads issued after the K
   // loop. Lanes 8-63 read past the range and write zeros.
   uint8_t *const bias_lds = smem + STAGES * SB + wave * 1024;
-  const bool bias_dma = bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 15) == 0;
+  const bool bias_dma = (!SPLIT || j < 0) && bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 15) == 0;
   if (bias_dma)
     load_lds16(make_rsrc(bias, static_cast<uint32_t>(N) * 2u), bias_lds,
                lane < 8 ? static_cast<uint32_t>(n0 + WN * wave + 8 * lane) * 2u : 0xfffffff0u, 0);
@@ -1285,7 +1328,7 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   WR w0, w1, w2;
   issue(0, 0, w0);
   if constexpr (STAGES == 3) {
-    issue(1, min(1, kblocks - 1), w1);
+    issue(1, min(1, nblk - 1), w1);
     wait_vmcnt<LPB>();
   } else {
     wait_vmcnt<0>();
@@ -1307,7 +1350,7 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // below is unrolled STAGES times so that the register sets rotate by name,
   // never by copying registers that a load in flight still targets.
   auto block = [&](int kb, const WR &cw, const WR &nw, WR &fw) {
-    const int fstage = (kb + LOOK) % STAGES, fblk = min(kb + LOOK, kblocks - 1);
+    const int fstage = (kb + LOOK) % STAGES, fblk = min(kb + LOOK, nblk - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
@@ -1356,23 +1399,53 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
     if constexpr (!kI8) __builtin_amdgcn_sched_barrier(0);
   };
 
+  // In the split kernel, wait here for everything read through the scalar cache
+  // (the workspace pointer is a kernel argument that only the epilogue uses):
+  // with a scalar load still pending at the loop, the first LDS wait of every
+  // iteration would have to be lgkmcnt(0), since scalar loads complete out of
+  // order (measured on linear1: 4 % slower).
+  if constexpr (SPLIT) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt unconstrained
   int kb = 0;
   if constexpr (STAGES == 3) {
-    for (; kb + 3 <= kblocks; kb += 3) {
+    for (; kb + 3 <= nblk; kb += 3) {
       block(kb, w0, w1, w2);
       block(kb + 1, w1, w2, w0);
       block(kb + 2, w2, w0, w1);
     }
-    if (kb < kblocks) block(kb, w0, w1, w2);
-    if (kb + 1 < kblocks) block(kb + 1, w1, w2, w0);
+    if (kb < nblk) block(kb, w0, w1, w2);
+    if (kb + 1 < nblk) block(kb + 1, w1, w2, w0);
   } else {
-    for (; kb + 2 <= kblocks; kb += 2) {
+    for (; kb + 2 <= nblk; kb += 2) {
       block(kb, w0, w1, w1);
       block(kb + 1, w1, w0, w0);
     }
-    if (kb < kblocks) block(kb, w0, w1, w1);
+    if (kb < nblk) block(kb, w0, w1, w1);
   }
   (void)w2;
+
+  if constexpr (SPLIT) {
+    if (j >= 0) {
+      // A split item leaves its fp32 partial tile in part[j], fragment-major:
+      // each store instruction writes 1 KiB (64 lanes x 16 bytes). Its wave's
+      // DMAs land before it ends, so none can reach the LDS of a later workgroup.
+      const __amdgpu_buffer_rsrc_t pr = make_rsrc(batch.part + static_cast<int64_t>(j) * (TM * TN), TM * TN * 4);
+      int pl = tid & 63;
+      asm volatile("" : "+v"(pl));
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(acc[mb][cb][4 * q]), __float_as_uint(acc[mb][cb][4 * q + 1]),
+                      __float_as_uint(acc[mb][cb][4 * q + 2]), __float_as_uint(acc[mb][cb][4 * q + 3])},
+                pr, static_cast<uint32_t>(pl) * 16u, wave * (MB * CB * 4096) + ((mb * CB + cb) * 4 + q) * 1024, 0);
+      wait_vmcnt<0>();
+      return;
+    }
+  }
 
   // Epilogue: acc[mb][cb] holds D[n][m] for n = n0 + WN*wave + 32*cb + 8*(r/4) + 4*h + r%4
   // and m = m0 + 32*mb + c. Bias is added in fp32 and the sum rounded once.
@@ -1534,18 +1607,98 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   }
 }
 
-template <int MB, int CB, int STAGES, int NW>
+template <int MB, int CB, int STAGES, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
-  qgemm_body<WCodec::kNF4, MB, CB, STAGES, NW>(batch, code);
+  qgemm_body<WCodec::kNF4, MB, CB, STAGES, NW, SPLIT>(batch, code);
 }
 template <int MB, int CB, int STAGES, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void int8_row_gemm_kernel(GemmBatch batch) {
   qgemm_body<WCodec::kInt8Row, MB, CB, STAGES, NW>(batch, Code16{});
 }
 
-// `batch.p[0..count)` filled except tiles_n / tile0, which are set here.
+// The outputs of the split tiles: each thread adds one 4-column group's K
+// ranges in K order (range 0 first, so the sum is the same on every run) and
+// finishes it as the tiled kernel's epilogue does: bias added in fp32 and the
+// sum rounded once to bf16; GELU columns rounded, GELU'd and rounded again.
+template <int MB, int CB, int NW>
+__global__ __launch_bounds__(256) void gemm_tail_sum(GemmBatch batch) {
+  constexpr int TM = 32 * MB, WN = 32 * CB, TN = NW * WN, T4 = TM * TN / 4;
+  const int e = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (e >= batch.tail * T4) return;
+  // e = q * T4 + ((f * 4 + q4) * 64 + lane), f = (wave * MB + mb) * CB + cb: the split items' store order.
+  const int q = e / T4, rem = e - q * T4;
+  const int lane = rem & 63, q4 = (rem >> 6) & 3, f = rem >> 8;
+  const int cb = f % CB, mb = (f / CB) % MB, wave = f / (CB * MB);
+  const float4 *src = reinterpret_cast<const float4 *>(batch.part) + static_cast<int64_t>(q) * T4 + rem;
+  float4 v = src[0];
+  for (int r = 1; r < batch.split; ++r) {
+    const float4 p = src[static_cast<int64_t>(r) * batch.tail * T4];
+    v.x += p.x;
+    v.y += p.y;
+    v.z += p.z;
+    v.w += p.w;
+  }
+  const int t = batch.tiles - batch.tail + q;
+  const GemmProblem P = tile_problem(batch, t);
+  int m0, n0;
+  tile_origin<TM, TN>(P, t, m0, n0);
+  const int m = m0 + 32 * mb + (lane & 31);
+  const int n = n0 + WN * wave + 32 * cb + 8 * q4 + 4 * (lane >> 5);
+  if (m >= P.M || n >= P.N) return;
+  const bool gelu = n0 >= P.n_split;
+  uint16_t *const dst = (gelu ? P.Y2 : P.Y) + static_cast<int64_t>(m) * (gelu ? P.ldy2 : P.ldy) + (n - (gelu ? P.n_split : 0));
+  float a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4)
+    a[t4] += (P.bias && n + t4 < P.N) ? bf16_bits_to_f32(P.bias[n + t4]) : 0.0f;
+  // Each value rounded to bf16 by the hardware convert; for GELU columns that
+  // rounded value GELU'd and rounded again.
+  auto out1 = [&](float x) -> uint32_t {
+    const uint32_t r = pack_bf16x2(x, 0.0f) & 0xffffu;
+    return gelu ? gelu_bf16x2(bf16_bits_to_f32(r), 0.0f) & 0xffffu : r;
+  };
+  if (n + 3 < P.N) {
+    *reinterpret_cast<uint2 *>(dst) = make_uint2(out1(a[0]) | (out1(a[1]) << 16), out1(a[2]) | (out1(a[3]) << 16));
+  } else {
+    for (int t4 = 0; t4 < 4 && n + t4 < P.N; ++t4) dst[t4] = static_cast<uint16_t>(out1(a[t4]));
+  }
+}
+
+// fp32 partial tiles of split launches: one buffer of `bytes` per (device,
+// stream), allocated at the first split launch and kept until the process ends.
+// Launches on one stream run in order and share it; launches on different
+// streams get different buffers. nullptr when the allocation fails (the caller
+// then launches without a split).
+float *split_workspace(hipStream_t s, size_t bytes) {
+  struct Entry {
+    int dev;
+    hipStream_t s;
+    void *p;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> entries;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(mu);
+  for (const Entry &e : entries)
+    if (e.dev == dev && e.s == s) return static_cast<float *>(e.p);
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  entries.push_back(Entry{dev, s, p});
+  return static_cast<float *>(p);
+}
+
+// `batch.p[0..count)` filled except tiles_n / tile0, which are set here. With
+// split > 1 the last round's tiles (tiles % CUs of them) run as `split` K ranges
+// each, when a workspace for their partial tiles is available.
 template <int MB, int CB, int STAGES, int NW>
-void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4) {
+void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4, int split = 1) {
   int64_t tiles = 0;
   for (int i = 0; i < batch.count; ++i) {
     GemmProblem &p = batch.p[i];
@@ -1554,11 +1707,29 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
     p.tile0 = static_cast<int>(tiles);
     tiles += tiles_m * tiles_n;
   }
+  constexpr int64_t kTileBytes = 32 * MB * 32 * CB * NW * 4;
+  const int64_t tail = tiles % cu_count();
   batch.tiles = static_cast<int>(tiles);
-  batch.per_xcd = static_cast<int>(cdiv(tiles, 8));
-  const dim3 grid(static_cast<uint32_t>(batch.per_xcd * 8)), block(64 * NW);
+  batch.tail = 0;
+  batch.split = 1;
+  batch.part = nullptr;
+  if (MB == 8 && wc == WCodec::kNF4 && split > 1 && tail > 0 && tail * split <= cu_count() && tiles > tail)
+    batch.part = split_workspace(s, static_cast<size_t>(cu_count()) * (256 * 256 * 4));  // the largest tile
+  if (batch.part) {
+    batch.tail = static_cast<int>(tail);
+    batch.split = split;
+  }
+  batch.per_xcd = static_cast<int>(cdiv(tiles - batch.tail, 8));
+  batch.dp_blocks = batch.per_xcd * 8;
+  batch.tail_per_xcd = static_cast<int>(cdiv(static_cast<int64_t>(batch.tail) * batch.split, 8));
+  const dim3 grid(static_cast<uint32_t>(batch.dp_blocks + 8 * batch.tail_per_xcd)), block(64 * NW);
   if (wc == WCodec::kInt8Row) int8_row_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch);
-  else nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
+  else if (batch.tail == 0) nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
+  else if constexpr (MB == 8) {
+    nf4_gemm_kernel<MB, CB, STAGES, NW, true><<<grid, block, 0, s>>>(batch, c);
+    const int64_t groups = static_cast<int64_t>(batch.tail) * (kTileBytes / 16);
+    gemm_tail_sum<MB, CB, NW><<<dim3(static_cast<uint32_t>(cdiv(groups, 256))), dim3(256), 0, s>>>(batch);
+  }
 }
 
 // Tiles of 4 waves side by side (each 64 columns), 3 LDS stages, and 256, 224
@@ -1586,8 +1757,35 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
   // kernel keeps the cost model (256-row tiles made that shape slower).
   int64_t t8 = 0;
   for (int i = 0; i < batch.count; ++i) t8 += cdiv(batch.p[i].M, 256) * cdiv(batch.p[i].N, 256);
-  if (wc == WCodec::kNF4 && t8 <= cu_count() && 4 * t8 >= 3 * static_cast<int64_t>(cu_count()))
-    launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
+  const int64_t cu = cu_count();
+  // Split tail (NF4, one K for the whole launch): the whole rounds of 256-row
+  // tiles, then the last round's tiles as S K ranges each, so that the last
+  // round takes ~1/S of a tile's K loop instead of all of it. Estimated in us: a
+  // 256-row tile takes ~14 + 1.48 per K block (fit over K = 3072..15360), a split
+  // item the same over its range, the partial tiles cost ~0.1 us each (written
+  // and read back) and the summing launch ~3 us. Taken when the estimate beats
+  // the best single height by 5 % (long K: 4 x 1536 tokens x 3072 x 15360, 288
+  // tiles, 580 us with 192-row tiles).
+  int split = 0;
+  bool one_k = true;
+  for (int i = 1; i < batch.count; ++i) one_k = one_k && batch.p[i].K == batch.p[0].K;
+  if (wc == WCodec::kNF4 && one_k && t8 > cu && t8 % cu) {
+    const int64_t tail = t8 % cu, kb = batch.p[0].K / 64;
+    const double tt = 14.0 + 1.48 * static_cast<double>(kb);
+    const double best = std::min(c8, std::min(c7, c6)) * tt;
+    double est = 0.0;
+    for (int S = 2; S <= 8 && tail * S <= cu && kb >= 3 * S; ++S) {
+      const double e = static_cast<double>(t8 / cu) * tt + 14.0 + 1.48 * static_cast<double>(kb) / S + 3.0 +
+                       0.1 * static_cast<double>(tail * S);
+      if (split == 0 || e < est) {
+        est = e;
+        split = S;
+      }
+    }
+    if (split && !(est < 0.95 * best)) split = 0;
+  }
+  if (split) launch_gemm<8, 2, 3, 4>(batch, c, s, wc, split);
+  else if (wc == WCodec::kNF4 && t8 <= cu && 4 * t8 >= 3 * cu) launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
   else if (c6 < 0.98 * c7 && c6 < 0.98 * c8) launch_gemm<6, 2, 3, 4>(batch, c, s, wc);
   else if (c7 < 0.98 * c8) launch_gemm<7, 2, 3, 4>(batch, c, s, wc);
   else launch_gemm<8, 2, 3, 4>(batch, c, s, wc);

@@ -143,8 +143,13 @@ def test_57_block_step_at_1024(flux):
 
 def test_batch4_512_step_equals_images_one_by_one(flux):
     # B4 at 512^2 (1024 image + 512 text tokens per image): every kernel works per token or per
-    # (image, head), so each image's velocity in the batch equals its velocity alone (to 1e-3: the raw
-    # global linears img_in / txt_in / final_layer run on the library GEMM, whose algorithm depends on M).
+    # (image, head), so each image's velocity in the batch equals its velocity alone up to the order of
+    # fp32 sums: the raw global linears img_in / txt_in / final_layer run on the library GEMM, whose
+    # algorithm depends on M, and at 4 x 1536 tokens the NF4 linears with K = 12288 and 15360 run their
+    # last round of tiles split over K (~6e-5 relative in the split tiles, which hold tokens of images 2
+    # and 3). Through 57 random-weight blocks that grows to 7.2e-3 for images 2 and 3 (5e-5 and 2e-5 for
+    # images 0 and 1; all four below 6e-5 without the split); an image reading another image's tokens or
+    # modulations would differ by O(1).
     dev = torch.device("cuda")
     run = F.FluxRunner(flux)
     g = seeded(46)
@@ -161,7 +166,7 @@ def test_batch4_512_step_equals_images_one_by_one(flux):
         ci = run.prepare(sig, 3.5, pooled[i:i + 1], txt[i:i + 1], F.image_ids(grid, grid), F.text_ids(lt))
         assert torch.equal(ci.mods["single.7"][:, 0], cond.mods["single.7"][:, i])  # per-image modulations
         vi, _ = run.step(s, lat[i:i + 1], ci)
-        assert rel(v[i:i + 1], vi) < 1e-3
+        assert rel(v[i:i + 1], vi) < 3e-2
 
 
 def test_runner_against_the_oracle_runner():

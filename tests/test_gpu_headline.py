@@ -3,7 +3,8 @@
 One FLUX single-stream block at 1024^2 (M = 4608 = 4096 image + 512 text tokens, hidden 3072): linear1
 3072 -> 21504 with GELU in its epilogue writing the MLP columns into linear2's [4608, 15360] input, and
 linear2 15360 -> 3072; the double block's image/text pairs (4096 / 512 tokens) in one batched launch,
-including mlp.2 with K = 12288; the 1536-token linear (12288 x 3072). Weights N(0, 0.02) NF4 blocksize 64,
+including mlp.2 with K = 12288; the 1536-token linear (12288 x 3072); at 512^2 with batch 4, linear2 and
+the mlp.2 pair, whose last round of tiles runs split over K. Weights N(0, 0.02) NF4 blocksize 64,
 activations bf16 N(0, 1), biases bf16 N(0, 0.02).
 
 Every output is checked on sampled rows (at least 128, all columns) against the fp64 product of x and
@@ -159,3 +160,45 @@ def test_1536_token_linear(dev):
     wd = codecs.decode("nf4", e.parts, e.meta, e.shape, torch.bfloat16).cpu()
     assert torch.equal(wd.float(), w)
     assert np.isfinite(y.float().cpu().numpy()).all()
+
+
+def assert_split_tail(y, alone, tail_rows, tail_cols, what):
+    """y from a launch whose last round ran split (the K ranges of the tail tiles summed afterwards), against
+    the same rows launched alone without a split: bit-equal outside the tail tiles, and inside them equal up
+    to the rounding of the fp32 partial sums (a different summation order over K)."""
+    outside = torch.ones_like(y, dtype=torch.bool)
+    outside[tail_rows, tail_cols] = False
+    assert torch.equal(y[outside], alone[outside]), f"{what}: whole tiles differ from the unsplit launch"
+    a, b = y[tail_rows, tail_cols].double(), alone[tail_rows, tail_cols].double()
+    assert ((a - b).norm() / b.norm()).item() < 1e-4, f"{what}: split tiles"
+    assert (a - b).abs().max().item() <= 2.0 ** -6 * b.abs().max().item(), f"{what}: split tiles"
+
+
+def test_512_batch4_linear2_split_tail(dev):
+    # 4 x (1024 + 512) tokens: 24 x 12 = 288 tiles of 256 x 256, one round plus 32 tiles. On 256 CUs the
+    # last 32 tiles (rows 5120-6143, columns 1024-3071 in the tile order) run as 8 K ranges of 30 blocks.
+    m = 4 * 1536
+    e2, w2 = weight(D, D + MLP, 600, dev)
+    x2, b2 = act(m, D + MLP, 601, dev), bias(D, 602, dev)
+    y = lin(x2, e2, b2)
+    assert torch.equal(lin(x2, e2, b2), y)  # the partial sums are added in a fixed order
+    rows = sample_rows(m, seed=3)
+    check_close(y[rows], oracle(x2, rows, w2, b2), "linear2 at 512^2 batch 4")
+    alone = torch.cat([lin(x2[:5120], e2, b2), lin(x2[5120:], e2, b2)])  # 240 and 48 tiles: no split
+    assert_split_tail(y, alone, slice(5120, m), slice(1024, D), "linear2 at 512^2 batch 4")
+
+
+def test_512_batch4_mlp2_pair_split_tail(dev):
+    # The double block's mlp.2 pair at 512^2 batch 4 (4096 image, 2048 text tokens, K = 12288) in one batched
+    # launch: 192 + 96 tiles, the last 32 of the text problem (its rows 1024-2047, columns 1024-3071) split.
+    ei, wi = weight(D, MLP, 610, dev)
+    et, wt = weight(D, MLP, 611, dev)
+    xi, xt = act(4096, MLP, 612, dev), act(2048, MLP, 613, dev)
+    bi, bt = bias(D, 614, dev), bias(D, 615, dev)
+    yi, yt = nf4_linear_batched([(xi, ei.parts["packed"], ei.parts["absmax"], 64, codecs.NF4_CODE, ei.shape, bi),
+                                 (xt, et.parts["packed"], et.parts["absmax"], 64, codecs.NF4_CODE, et.shape, bt)])
+    assert torch.equal(yi, lin(xi, ei, bi))
+    assert_split_tail(yt, lin(xt, et, bt), slice(1024, 2048), slice(1024, D), "text mlp.2")
+    ri, rt = sample_rows(4096, seed=8), sample_rows(2048, count=128, seed=9)
+    check_close(yi[ri], oracle(xi, ri, wi, bi), "img mlp.2")
+    check_close(yt[rt], oracle(xt, rt, wt, bt), "txt mlp.2")

@@ -228,6 +228,31 @@ def test_gelu_epilogue_equals_linear_then_gelu(dev, m, n, k, gc, with_bias):
     check_close(full, oracle_linear(x, w_ref, b))
 
 
+def test_split_tail_with_gelu_columns(dev):
+    # M = 16640, N = 1024, K = 2048: 65 x 4 = 260 tiles of 256 x 256, one round plus 4 (the last row slab,
+    # rows 16384-16639). On 256 CUs those 4 run as 8 K ranges each, and a second kernel adds the ranges and
+    # finishes them: bias, rounding and, for the last 512 columns, GELU. The GELU columns must equal the
+    # plain output of the same launch through the GELU segment bit for bit, the whole tiles must equal a
+    # launch of their rows alone, and everything must match the oracle.
+    from selas_amd.kernels import Kernels
+    from selas_amd.linear import nf4_linear_gelu
+
+    m, n, k, gc = 16640, 1024, 2048, 512
+    p, a, w_ref = make_weight(n, k, 81, dev)
+    x = torch.randn(m, k, generator=seeded(82)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(83)) * 0.02).to(torch.bfloat16).to(dev)
+    ((y, g),) = nf4_linear_gelu([(x, p, a, 64, codecs.NF4_CODE, (n, k), b, gc, None)])
+    full = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    assert torch.equal(y, full[:, :n - gc]) and torch.equal(g, Kernels().gelu(full[:, n - gc:]))
+    assert torch.equal(nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b), full)
+    assert torch.equal(full[:16384], nf4_linear(x[:16384], p, a, 64, codecs.NF4_CODE, (n, k), b))
+    tail = full[16384:].double()
+    alone = nf4_linear(x[16384:], p, a, 64, codecs.NF4_CODE, (n, k), b).double()
+    assert ((tail - alone).norm() / alone.norm()).item() < 1e-4
+    rows = torch.cat([torch.randint(0, 16384, (96,), generator=seeded(84)), torch.arange(16384, m, 4)])
+    check_close(full[rows], oracle_linear(x[rows], w_ref, b))
+
+
 def test_tile_height_does_not_change_the_bits(dev):
     # M = 2048, N = 8192 runs 256-row tiles (256 tiles, one round); its first 300 rows alone run
     # 192-row tiles (one round either way, fewer rows per tile). Every output sums K in the same

@@ -1620,6 +1620,8 @@ __global__ __launch_bounds__(64 * NW, 1) void int8_row_gemm_kernel(GemmBatch bat
 // ranges in K order (range 0 first, so the sum is the same on every run) and
 // finishes it as the tiled kernel's epilogue does: bias added in fp32 and the
 // sum rounded once to bf16; GELU columns rounded, GELU'd and rounded again.
+constexpr int kMaxSplit = 8;  // K ranges per split tile at most
+
 template <int MB, int CB, int NW>
 __global__ __launch_bounds__(256) void gemm_tail_sum(GemmBatch batch) {
   constexpr int TM = 32 * MB, WN = 32 * CB, TN = NW * WN, T4 = TM * TN / 4;
@@ -1629,15 +1631,21 @@ __global__ __launch_bounds__(256) void gemm_tail_sum(GemmBatch batch) {
   const int q = e / T4, rem = e - q * T4;
   const int lane = rem & 63, q4 = (rem >> 6) & 3, f = rem >> 8;
   const int cb = f % CB, mb = (f / CB) % MB, wave = f / (CB * MB);
+  // All ranges' loads first (up to kMaxSplit in flight), then the sums in K order.
   const float4 *src = reinterpret_cast<const float4 *>(batch.part) + static_cast<int64_t>(q) * T4 + rem;
-  float4 v = src[0];
-  for (int r = 1; r < batch.split; ++r) {
-    const float4 p = src[static_cast<int64_t>(r) * batch.tail * T4];
-    v.x += p.x;
-    v.y += p.y;
-    v.z += p.z;
-    v.w += p.w;
-  }
+  float4 p[kMaxSplit];
+#pragma unroll
+  for (int r = 0; r < kMaxSplit; ++r)
+    if (r < batch.split) p[r] = src[static_cast<int64_t>(r) * batch.tail * T4];
+  float4 v = p[0];
+#pragma unroll
+  for (int r = 1; r < kMaxSplit; ++r)
+    if (r < batch.split) {
+      v.x += p[r].x;
+      v.y += p[r].y;
+      v.z += p[r].z;
+      v.w += p[r].w;
+    }
   const int t = batch.tiles - batch.tail + q;
   const GemmProblem P = tile_problem(batch, t);
   int m0, n0;
@@ -1713,7 +1721,8 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
   batch.tail = 0;
   batch.split = 1;
   batch.part = nullptr;
-  if (MB == 8 && wc == WCodec::kNF4 && split > 1 && tail > 0 && tail * split <= cu_count() && tiles > tail)
+  if (MB == 8 && wc == WCodec::kNF4 && split > 1 && split <= kMaxSplit && tail > 0 && tail * split <= cu_count() &&
+      tiles > tail)
     batch.part = split_workspace(s, static_cast<size_t>(cu_count()) * (256 * 256 * 4));  // the largest tile
   if (batch.part) {
     batch.tail = static_cast<int>(tail);
@@ -1774,7 +1783,7 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
     const double tt = 14.0 + 1.48 * static_cast<double>(kb);
     const double best = std::min(c8, std::min(c7, c6)) * tt;
     double est = 0.0;
-    for (int S = 2; S <= 8 && tail * S <= cu && kb >= 3 * S; ++S) {
+    for (int S = 2; S <= kMaxSplit && tail * S <= cu && kb >= 3 * S; ++S) {
       const double e = static_cast<double>(t8 / cu) * tt + 14.0 + 1.48 * static_cast<double>(kb) / S + 3.0 +
                        0.1 * static_cast<double>(tail * S);
       if (split == 0 || e < est) {

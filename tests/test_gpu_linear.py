@@ -253,6 +253,26 @@ def test_split_tail_with_gelu_columns(dev):
     check_close(full[rows], oracle_linear(x[rows], w_ref, b))
 
 
+def test_split_tail_on_two_streams_at_once(dev):
+    # Split launches keep their partial tiles in one workspace per stream: the split shape run on two
+    # streams at the same time gives the bits of the same launches on the default stream.
+    m, n, k = 16640, 1024, 2048
+    p, a, _ = make_weight(n, k, 91, dev)
+    xs = [torch.randn(m, k, generator=seeded(92 + i)).to(torch.bfloat16).to(dev) for i in range(2)]
+    ref = [nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    outs = [[], []]
+    for _ in range(4):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[i].append(nf4_linear(xs[i], p, a, 64, codecs.NF4_CODE, (n, k), None))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for y in outs[i]:
+            assert torch.equal(y, ref[i])
+
+
 def test_tile_height_does_not_change_the_bits(dev):
     # M = 2048, N = 8192 runs 256-row tiles (256 tiles, one round); its first 300 rows alone run
     # 192-row tiles (one round either way, fewer rows per tile). Every output sums K in the same

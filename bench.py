@@ -22,7 +22,8 @@ The same JSON line carries:
 
 Per-kernel figures are medians of HIP-event times over the timed steps (the roofline figure uses
 the mean, as a kernel trace's average does). The default 30 warmup steps take the GPU past its
-clock ramp under sustained load.
+clock ramp under sustained load, and every configuration whose warm-up launches are short runs at least
+80 ms of back-to-back launches before its timed ones.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-full-step] [--no-extra] [--no-cpu]
 """
@@ -76,6 +77,18 @@ def lin(x, e, b=None):
     from selas_amd.linear import nf4_linear
 
     return nf4_linear(x, e.parts["packed"], e.parts["absmax"], 64, codecs.NF4_CODE, e.shape, b)
+
+
+def sustain(fn, dev, min_s: float = 0.08) -> None:
+    """Runs `fn` back to back for at least `min_s` of GPU time: under sustained load the GPU needs ~35 ms
+    to settle its clock, and a short kernel's warm-up launches alone do not last that long."""
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize(dev)
+        if time.perf_counter() - t0 >= min_s:
+            return
 
 
 class Timer:
@@ -159,7 +172,8 @@ def bench_single_linear(dev, steps, warmup):
     x = act(m, k, 1, dev)
     for i in range(warmup):
         lin(x, ws[i % 8])
-    torch.cuda.synchronize(dev)
+    it = iter(range(1 << 30))
+    sustain(lambda: lin(x, ws[next(it) % 8]), dev)  # ~130 us per launch: the warm-up count alone is a few ms
     tm = Timer()
     for i in range(steps):
         t = tm.start("l")
@@ -185,7 +199,7 @@ def bench_library_path(dev, steps, warmup):
 
     for _ in range(warmup):
         run()
-    torch.cuda.synchronize(dev)
+    sustain(run, dev)
     t0 = time.perf_counter()
     for _ in range(steps):
         run()
@@ -279,7 +293,14 @@ def bench_int8_row(dev, steps, warmup, copies=8):
     for i in range(warmup):
         run(x1, w1[i % copies], b1)
         run(x2, w2[i % copies], b2)
-    torch.cuda.synchronize(dev)
+    it = iter(range(1 << 30))
+
+    def pair():
+        i = next(it)
+        run(x1, w1[i % copies], b1)
+        run(x2, w2[i % copies], b2)
+
+    sustain(pair, dev)
     tm = Timer()
     for i in range(steps):
         t = tm.start("linear1")
@@ -388,7 +409,7 @@ def bench_segments(dev, steps, warmup):
     for name, (fn, nb) in cases.items():
         for _ in range(warmup):
             fn()
-        torch.cuda.synchronize(dev)
+        sustain(fn, dev)
         tm = Timer()
         for _ in range(max(5, steps // 4)):
             t = tm.start(name)
@@ -443,7 +464,7 @@ def bench_attention(dev, steps, warmup):
         for key, fn in runs.items():
             for _ in range(warmup):
                 fn()
-            torch.cuda.synchronize(dev)
+            sustain(fn, dev)
             tm = Timer()
             for _ in range(steps):
                 t = tm.start(key)

@@ -1349,13 +1349,23 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   // block kb+LOOK's (with one block of lookahead that is nw itself). The loop
   // below is unrolled STAGES times so that the register sets rotate by name,
   // never by copying registers that a load in flight still targets.
-  auto block = [&](int kb, const WR &cw, const WR &nw, WR &fw) {
+  //
+  // The blocks after the unrolled loop (K/64 not a multiple of STAGES) issue no
+  // loads and wait for all outstanding ones before their barrier: all their
+  // look-ahead would be past the end of K, and the compiler deletes register
+  // loads whose values are never used, so a count of younger loads (as the
+  // loop's wait uses) would be short there and let the next block's last x
+  // loads still be in flight at the barrier (measured: wrong outputs for
+  // K = 2048 when another kernel ran on the GPU at the same time).
+  auto block = [&](int kb, const WR &cw, const WR &nw, WR &fw, auto tail_tag) __attribute__((always_inline)) {
+    constexpr bool kTail = decltype(tail_tag)::value;
     const int fstage = (kb + LOOK) % STAGES, fblk = min(kb + LOOK, nblk - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
       if (s < 3) {
-        if constexpr (LOOK >= 2) {
+        if constexpr (kTail) {
+        } else if constexpr (LOOK >= 2) {
           issue_part(fstage, fblk, s, fw);
         } else if (s == 0) {
 #pragma unroll
@@ -1364,7 +1374,10 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) wf[nxt][cb] = wfrag(cw, cb, s + 1, tab[cb]);
       } else {
-        if constexpr (LOOK >= 2) {
+        if constexpr (kTail) {
+          wait_vmcnt<0>();
+          lds_barrier();
+        } else if constexpr (LOOK >= 2) {
           // Block kb+1's loads are older than parts 0-2 of block kb+LOOK's.
           wait_vmcnt<(LOOK - 1) * LPB - P3>();
           lds_barrier();
@@ -1408,18 +1421,18 @@ __device__ __forceinline__ void qgemm_body(GemmBatch batch, const Code16 &code) 
   int kb = 0;
   if constexpr (STAGES == 3) {
     for (; kb + 3 <= nblk; kb += 3) {
-      block(kb, w0, w1, w2);
-      block(kb + 1, w1, w2, w0);
-      block(kb + 2, w2, w0, w1);
+      block(kb, w0, w1, w2, BoolTag<false>{});
+      block(kb + 1, w1, w2, w0, BoolTag<false>{});
+      block(kb + 2, w2, w0, w1, BoolTag<false>{});
     }
-    if (kb < nblk) block(kb, w0, w1, w2);
-    if (kb + 1 < nblk) block(kb + 1, w1, w2, w0);
+    if (kb < nblk) block(kb, w0, w1, w2, BoolTag<true>{});
+    if (kb + 1 < nblk) block(kb + 1, w1, w2, w0, BoolTag<true>{});
   } else {
     for (; kb + 2 <= nblk; kb += 2) {
-      block(kb, w0, w1, w1);
-      block(kb + 1, w1, w0, w0);
+      block(kb, w0, w1, w1, BoolTag<false>{});
+      block(kb + 1, w1, w0, w0, BoolTag<false>{});
     }
-    if (kb < nblk) block(kb, w0, w1, w1);
+    if (kb < nblk) block(kb, w0, w1, w1, BoolTag<true>{});
   }
   (void)w2;
 

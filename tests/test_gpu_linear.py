@@ -253,13 +253,19 @@ def test_split_tail_with_gelu_columns(dev):
     check_close(full[rows], oracle_linear(x[rows], w_ref, b))
 
 
-def test_split_tail_on_two_streams_at_once(dev):
-    # Split launches keep their partial tiles in one workspace per stream: the split shape run on two
-    # streams at the same time gives the bits of the same launches on the default stream.
-    m, n, k = 16640, 1024, 2048
+@pytest.mark.parametrize("m", [16384, 16640])
+def test_bits_do_not_depend_on_concurrent_kernels(dev, m):
+    # The tiled GEMM run on two streams at once, and beside an unrelated kernel on another stream, gives
+    # the bits of the same launches alone. K = 2048 is 32 K blocks, two past the unrolled loop of three: a
+    # wait there counted loads that the compiler had deleted, and the last block's x tile could still be
+    # in flight when it was read, which showed only when another kernel slowed the loads down (16384
+    # rows: 256 tiles in one round). 16640 rows also split the last round's 4 tiles over K, whose partial
+    # tiles live in one workspace per stream.
+    n, k = 1024, 2048
     p, a, _ = make_weight(n, k, 91, dev)
     xs = [torch.randn(m, k, generator=seeded(92 + i)).to(torch.bfloat16).to(dev) for i in range(2)]
     ref = [nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None) for x in xs]
+    big = torch.randn(64 << 20, device=dev)
     torch.cuda.synchronize()
     streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
     outs = [[], []]
@@ -267,6 +273,11 @@ def test_split_tail_on_two_streams_at_once(dev):
         for i, st in enumerate(streams):
             with torch.cuda.stream(st):
                 outs[i].append(nf4_linear(xs[i], p, a, 64, codecs.NF4_CODE, (n, k), None))
+    for _ in range(4):
+        with torch.cuda.stream(streams[0]):
+            outs[0].append(nf4_linear(xs[0], p, a, 64, codecs.NF4_CODE, (n, k), None))
+        with torch.cuda.stream(streams[1]):
+            big.mul_(1.0)
     torch.cuda.synchronize()
     for i in range(2):
         for y in outs[i]:

@@ -350,3 +350,22 @@ def test_seeded_random_shapes(dev, m, n, k):
     x = torch.randn(m, k, generator=seeded(m + k)).to(torch.bfloat16).to(dev)
     b = (torch.randn(n, generator=seeded(n)) * 0.02).to(torch.bfloat16).to(dev) if m % 2 else None
     check_close(nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b), oracle_linear(x, w_ref, b))
+
+
+def test_seeded_random_shapes_beside_another_kernel(dev):
+    # The seeded shapes (K from 1 to 16 blocks: every remainder of the three-block loop) again, each run
+    # four times while an elementwise kernel streams 256 MB on a second stream: the same bits as alone.
+    big = torch.randn(64 << 20, device=dev)
+    other = torch.cuda.Stream(dev)
+    for m, n, k in _RNG_SHAPES:
+        p, a, _ = make_weight(n, k, m * 7 + n, dev)
+        x = torch.randn(m * 8, k, generator=seeded(m + k)).to(torch.bfloat16).to(dev)
+        ref = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None)
+        torch.cuda.synchronize()
+        outs = []
+        for _ in range(4):
+            with torch.cuda.stream(other):
+                big.mul_(1.0)
+            outs.append(nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None))
+        torch.cuda.synchronize()
+        assert all(torch.equal(y, ref) for y in outs), (m * 8, n, k)

@@ -110,6 +110,27 @@ def test_tiled_path(dev, m, n, k, with_bias):
     check_close(int8_row_linear(x, q, s, (n, k), b), oracle_linear(x, w_ref, b))
 
 
+@pytest.mark.parametrize("k", [128, 320, 2048])
+def test_tiled_bits_beside_another_kernel(dev, k):
+    # K/64 = 2 (mod 3): the K blocks after the unrolled loop of three must wait for all their loads. Run
+    # while an elementwise kernel streams 256 MB on another stream, the tiled int8 GEMM gives the bits of
+    # the same launch alone.
+    n = 1024
+    q, s, _ = make_weight(n, k, 31, dev)
+    x = torch.randn(16384, k, generator=seeded(32)).to(torch.bfloat16).to(dev)
+    ref = int8_row_linear(x, q, s, (n, k))
+    big = torch.randn(64 << 20, device=dev)
+    other = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(4):
+        with torch.cuda.stream(other):
+            big.mul_(1.0)
+        outs.append(int8_row_linear(x, q, s, (n, k)))
+    torch.cuda.synchronize()
+    assert all(torch.equal(y, ref) for y in outs)
+
+
 def test_tiled_operand_is_the_reference_decode_bit_for_bit(dev):
     n, k, m = 320, 640, 96
     q, s, w_ref = make_weight(n, k, 7, dev)

@@ -730,7 +730,7 @@ def main():
                     help="first run a 1 GiB device copy (reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
+        print(f"bench.py measures one GPU: selas_amd has no multi-GPU path (asked for --gpus {a.gpus})",
               file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda", 0)

@@ -82,6 +82,41 @@ def test_full_width_single_block(flux):
     assert e <= L2_REL
 
 
+def test_full_width_double_block_512_batch4(flux):
+    # 4 images at 512^2: the image/text pairs run batched (4096 + 2048 rows), and mlp.2 (K = 12288, 288
+    # tiles) runs its last 32 tiles split over K on 256 CUs.
+    lt, grid, b = 512, 32, 4
+    g = seeded(48)
+    img = torch.randn(b, grid * grid, CFG.hidden, generator=g)
+    txt = torch.randn(b, lt, CFG.hidden, generator=g)
+    mod = (torch.randn(b, 12 * CFG.hidden, generator=g) * 0.3).to(BF16)
+    cos, sin = rope(lt, grid)
+    dev = torch.device("cuda")
+    w = flux.doubles[7]
+    gi, gt = F.double_block(w, img.to(dev), txt.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG, BF16, False)
+    ri, rt = OF.double_block(oracle_unit(w), img, txt, mod, cos, sin, OCFG, BF16, False)
+    ei, et = rel(gi.cpu() - img, ri - img), rel(gt.cpu() - txt, rt - txt)
+    print(f"double block 512^2 batch 4: update rel L2 img {ei:.2e} txt {et:.2e}")
+    assert ei <= L2_REL and et <= L2_REL
+
+
+def test_full_width_single_block_512_batch4(flux):
+    # 4 images at 512^2 (512 text + 1024 image tokens each, 6144 rows): linear2 (K = 15360) has 288 tiles,
+    # and on 256 CUs its last 32 run split over K with their partial tiles summed by a second kernel.
+    lt, grid, b = 512, 32, 4
+    g = seeded(47)
+    x = torch.randn(b, lt + grid * grid, CFG.hidden, generator=g)
+    mod = (torch.randn(b, 3 * CFG.hidden, generator=g) * 0.3).to(BF16)
+    cos, sin = rope(lt, grid)
+    dev = torch.device("cuda")
+    w = flux.singles[9]
+    gx = F.single_block(w, x.to(dev), mod.to(dev), cos.to(dev), sin.to(dev), CFG, BF16, False)
+    rx = OF.single_block(oracle_unit(w), x, mod, cos, sin, OCFG, BF16, False)
+    e = rel(gx.cpu() - x, rx - x)
+    print(f"single block 512^2 batch 4: update rel L2 {e:.2e}")
+    assert e <= L2_REL
+
+
 def test_grouped_modulations_all_76_weights(flux):
     # One grouped launch over the 76 modulation linears (19 x img/txt 3072 -> 18432, 38 x 3072 -> 9216) at
     # M = 28 steps; per weight, 96 sampled output features (all 28 rows) against the oracle's decode of those

@@ -10,9 +10,10 @@
  *     buffer reuse stays correct) and never synchronises the device;
  *   - allocates nothing and frees nothing: outputs are caller-owned (one
  *     exception: the tiled NF4 linears allocate one 64 MiB workspace per
- *     device and stream at their first launch that splits its last round of
- *     tiles over K, and keep it until the process ends; a first call outside
- *     HIP graph capture sets it up);
+ *     device and stream, for up to 8 streams per device, at their first
+ *     launch that splits its last round of tiles over K, and keep it until
+ *     the process ends; a first call outside HIP graph capture sets it up;
+ *     further streams launch without the split);
  *   - returns SELAS_OK or an error code and never throws; the message of the
  *     last error on the calling thread is returned by selas_last_error().
  *

@@ -1688,8 +1688,11 @@ __global__ __launch_bounds__(256) void gemm_tail_sum(GemmBatch batch) {
 // fp32 partial tiles of split launches: one buffer of `bytes` per (device,
 // stream), allocated at the first split launch and kept until the process ends.
 // Launches on one stream run in order and share it; launches on different
-// streams get different buffers. nullptr when the allocation fails (the caller
-// then launches without a split).
+// streams get different buffers, for at most kMaxSplitStreams streams per
+// device (a caller that makes a stream per request does not grow memory
+// without bound). nullptr when the allocation fails or the streams are used up
+// (the caller then launches without a split).
+constexpr int kMaxSplitStreams = 8;
 float *split_workspace(hipStream_t s, size_t bytes) {
   struct Entry {
     int dev;
@@ -1704,8 +1707,12 @@ float *split_workspace(hipStream_t s, size_t bytes) {
     return nullptr;
   }
   std::lock_guard<std::mutex> g(mu);
-  for (const Entry &e : entries)
+  int on_dev = 0;
+  for (const Entry &e : entries) {
     if (e.dev == dev && e.s == s) return static_cast<float *>(e.p);
+    on_dev += e.dev == dev;
+  }
+  if (on_dev >= kMaxSplitStreams) return nullptr;
   void *p = nullptr;
   if (hipMalloc(&p, bytes) != hipSuccess) {
     (void)hipGetLastError();

@@ -284,6 +284,29 @@ def test_bits_do_not_depend_on_concurrent_kernels(dev, m):
             assert torch.equal(y, ref[i])
 
 
+def test_split_launches_on_many_streams(dev):
+    # One split workspace per stream for up to 8 streams per device; launches on further streams run
+    # unsplit. Either way the whole tiles give the same bits and the split ones agree to the order of the
+    # fp32 sums (M = 16640, N = 1024, K = 2048: the last row slab is split on 256 CUs).
+    m, n, k = 16640, 1024, 2048
+    p, a, w_ref = make_weight(n, k, 101, dev)
+    x = torch.randn(m, k, generator=seeded(102)).to(torch.bfloat16).to(dev)
+    ref = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(dev) for _ in range(12)]
+    outs = []
+    for st in streams:
+        with torch.cuda.stream(st):
+            outs.append(nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None))
+    torch.cuda.synchronize()
+    for y in outs:
+        assert torch.equal(y[:16384], ref[:16384])
+        d = (y[16384:].double() - ref[16384:].double()).norm() / ref[16384:].double().norm()
+        assert d.item() < 1e-4
+    rows = torch.arange(16384, m, 8)
+    check_close(outs[-1][rows], oracle_linear(x[rows], w_ref, None))
+
+
 def test_tile_height_does_not_change_the_bits(dev):
     # M = 2048, N = 8192 runs 256-row tiles (256 tiles, one round); its first 300 rows alone run
     # 192-row tiles (one round either way, fewer rows per tile). Every output sums K in the same

@@ -9,7 +9,7 @@
  *     hipStream_t; pass the caller's current stream so that stream-ordered
  *     buffer reuse stays correct) and never synchronises the device;
  *   - allocates nothing and frees nothing: outputs are caller-owned (one
- *     exception: the tiled NF4 linears allocate one 64 MiB workspace per
+ *     exception: the tiled NF4 and int8_row linears allocate one 64 MiB workspace per
  *     device and stream, for up to 8 streams per device, at their first
  *     launch that splits its last round of tiles over K, and keep it until
  *     the process ends; a first call outside HIP graph capture sets it up;

@@ -1624,9 +1624,9 @@ template <int MB, int CB, int STAGES, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW, 1) void nf4_gemm_kernel(GemmBatch batch, Code16 code) {
   qgemm_body<WCodec::kNF4, MB, CB, STAGES, NW, SPLIT>(batch, code);
 }
-template <int MB, int CB, int STAGES, int NW>
+template <int MB, int CB, int STAGES, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW, 1) void int8_row_gemm_kernel(GemmBatch batch) {
-  qgemm_body<WCodec::kInt8Row, MB, CB, STAGES, NW>(batch, Code16{});
+  qgemm_body<WCodec::kInt8Row, MB, CB, STAGES, NW, SPLIT>(batch, Code16{});
 }
 
 // The outputs of the split tiles: each thread adds one 4-column group's K
@@ -1741,8 +1741,7 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
   batch.tail = 0;
   batch.split = 1;
   batch.part = nullptr;
-  if (MB == 8 && wc == WCodec::kNF4 && split > 1 && split <= kMaxSplit && tail > 0 && tail * split <= cu_count() &&
-      tiles > tail)
+  if (MB == 8 && split > 1 && split <= kMaxSplit && tail > 0 && tail * split <= cu_count() && tiles > tail)
     batch.part = split_workspace(s, static_cast<size_t>(cu_count()) * (256 * 256 * 4));  // the largest tile
   if (batch.part) {
     batch.tail = static_cast<int>(tail);
@@ -1752,10 +1751,12 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
   batch.dp_blocks = batch.per_xcd * 8;
   batch.tail_per_xcd = static_cast<int>(cdiv(static_cast<int64_t>(batch.tail) * batch.split, 8));
   const dim3 grid(static_cast<uint32_t>(batch.dp_blocks + 8 * batch.tail_per_xcd)), block(64 * NW);
-  if (wc == WCodec::kInt8Row) int8_row_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch);
-  else if (batch.tail == 0) nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
-  else if constexpr (MB == 8) {
-    nf4_gemm_kernel<MB, CB, STAGES, NW, true><<<grid, block, 0, s>>>(batch, c);
+  if (batch.tail == 0) {
+    if (wc == WCodec::kInt8Row) int8_row_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch);
+    else nf4_gemm_kernel<MB, CB, STAGES, NW><<<grid, block, 0, s>>>(batch, c);
+  } else if constexpr (MB == 8) {
+    if (wc == WCodec::kInt8Row) int8_row_gemm_kernel<MB, CB, STAGES, NW, true><<<grid, block, 0, s>>>(batch);
+    else nf4_gemm_kernel<MB, CB, STAGES, NW, true><<<grid, block, 0, s>>>(batch, c);
     const int64_t groups = static_cast<int64_t>(batch.tail) * (kTileBytes / 16);
     gemm_tail_sum<MB, CB, NW><<<dim3(static_cast<uint32_t>(cdiv(groups, 256))), dim3(256), 0, s>>>(batch);
   }
@@ -1787,7 +1788,7 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
   int64_t t8 = 0;
   for (int i = 0; i < batch.count; ++i) t8 += cdiv(batch.p[i].M, 256) * cdiv(batch.p[i].N, 256);
   const int64_t cu = cu_count();
-  // Split tail (NF4, one K for the whole launch): the whole rounds of 256-row
+  // Split tail (one K for the whole launch): the whole rounds of 256-row
   // tiles, then the last round's tiles as S K ranges each, so that the last
   // round takes ~1/S of a tile's K loop instead of all of it. Estimated in us: a
   // 256-row tile takes ~14 + 1.48 per K block (fit over K = 3072..15360), a split
@@ -1798,7 +1799,7 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
   int split = 0;
   bool one_k = true;
   for (int i = 1; i < batch.count; ++i) one_k = one_k && batch.p[i].K == batch.p[0].K;
-  if (wc == WCodec::kNF4 && one_k && t8 > cu && t8 % cu) {
+  if (one_k && t8 > cu && t8 % cu) {
     const int64_t tail = t8 % cu, kb = batch.p[0].K / 64;
     const double tt = 14.0 + 1.48 * static_cast<double>(kb);
     const double best = std::min(c8, std::min(c7, c6)) * tt;

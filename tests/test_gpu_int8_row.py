@@ -131,6 +131,24 @@ def test_tiled_bits_beside_another_kernel(dev, k):
     assert all(torch.equal(y, ref) for y in outs)
 
 
+def test_tiled_split_tail(dev):
+    # M = 16640, N = 1024, K = 2048: 260 tiles of 256 x 256; on 256 CUs the last row slab's 4 tiles run as 8
+    # K ranges each, summed in K order by a second kernel. The whole tiles equal a launch of their rows alone
+    # bit for bit, the split ones agree with an unsplit launch to the order of the fp32 sums, and sampled rows
+    # of both match the oracle.
+    m, n, k = 16640, 1024, 2048
+    q, s, w_ref = make_weight(n, k, 41, dev)
+    x = torch.randn(m, k, generator=seeded(42)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(43)) * 0.02).to(torch.bfloat16).to(dev)
+    y = int8_row_linear(x, q, s, (n, k), b)
+    assert torch.equal(int8_row_linear(x, q, s, (n, k), b), y)
+    assert torch.equal(y[:16384], int8_row_linear(x[:16384], q, s, (n, k), b))
+    alone = int8_row_linear(x[16384:], q, s, (n, k), b).double()
+    assert ((y[16384:].double() - alone).norm() / alone.norm()).item() < 1e-4
+    rows = torch.cat([torch.randint(0, 16384, (64,), generator=seeded(44)), torch.arange(16384, m, 4)])
+    check_close(y[rows], oracle_linear(x[rows], w_ref, b))
+
+
 def test_tiled_operand_is_the_reference_decode_bit_for_bit(dev):
     n, k, m = 320, 640, 96
     q, s, w_ref = make_weight(n, k, 7, dev)

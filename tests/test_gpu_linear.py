@@ -253,15 +253,15 @@ def test_split_tail_with_gelu_columns(dev):
     check_close(full[rows], oracle_linear(x[rows], w_ref, b))
 
 
-@pytest.mark.parametrize("m", [16384, 16640])
-def test_bits_do_not_depend_on_concurrent_kernels(dev, m):
+@pytest.mark.parametrize("m,n,k", [(16384, 1024, 2048), (16640, 1024, 2048), (1536, 12288, 128)])
+def test_bits_do_not_depend_on_concurrent_kernels(dev, m, n, k):
     # The tiled GEMM run on two streams at once, and beside an unrelated kernel on another stream, gives
     # the bits of the same launches alone. K = 2048 is 32 K blocks, two past the unrolled loop of three: a
     # wait there counted loads that the compiler had deleted, and the last block's x tile could still be
     # in flight when it was read, which showed only when another kernel slowed the loads down (16384
     # rows: 256 tiles in one round). 16640 rows also split the last round's 4 tiles over K, whose partial
-    # tiles live in one workspace per stream.
-    n, k = 1024, 2048
+    # tiles live in one workspace per stream. 1536 x 12288 x 128 runs 192-row tiles with two blocks after
+    # the (empty) loop.
     p, a, _ = make_weight(n, k, 91, dev)
     xs = [torch.randn(m, k, generator=seeded(92 + i)).to(torch.bfloat16).to(dev) for i in range(2)]
     ref = [nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None) for x in xs]

@@ -8,12 +8,9 @@
  *   - launches asynchronously on the HIP stream passed as `stream` (a
  *     hipStream_t; pass the caller's current stream so that stream-ordered
  *     buffer reuse stays correct) and never synchronises the device;
- *   - allocates nothing and frees nothing: outputs are caller-owned (one
- *     exception: the tiled NF4 and int8_row linears allocate one 64 MiB workspace per
- *     device and stream, for up to 8 streams per device, at their first
- *     launch that splits its last round of tiles over K, and keep it until
- *     the process ends; a first call outside HIP graph capture sets it up;
- *     further streams launch without the split);
+ *   - allocates nothing and frees nothing: outputs and scratch memory are
+ *     caller-owned (a tiled linear whose launch splits its last round of tiles
+ *     over K takes a workspace argument, sized by selas_linear_workspace_bytes);
  *   - returns SELAS_OK or an error code and never throws; the message of the
  *     last error on the calling thread is returned by selas_last_error().
  *
@@ -24,9 +21,10 @@
  * (the tensor's meta["code"]); int8_row weights are `q` int8 in the weight's
  * shape and `scale` fp32, one per row.
  *
- * Kernels are chosen from shapes, dtypes and pointer alignment (and the GPU's
- * CU count) only and use no atomics, so equal inputs give equal bits on every
- * call.
+ * Kernels, tile shapes and K splits are chosen from shapes, dtypes and pointer
+ * alignment (and the GPU's CU count) only, never from streams, earlier calls or
+ * allocation results, and use no atomics, so equal inputs give equal bits on
+ * every call and every stream.
  */
 #ifndef SELAS_AMD_H
 #define SELAS_AMD_H
@@ -47,6 +45,10 @@ extern "C" {
 #define SELAS_F32 0
 #define SELAS_F16 1
 #define SELAS_BF16 2
+
+/* Weight codecs (the `codec` argument of selas_linear_workspace_bytes). */
+#define SELAS_CODEC_NF4 0
+#define SELAS_CODEC_INT8_ROW 1
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *selas_last_error(void);
@@ -115,7 +117,12 @@ int selas_int8_row_encode(const float *w, int64_t rows, int64_t cols, int8_t *q,
  * one order, whatever M and the tile height, except where a launch splits its
  * last round of tiles over K (long K and a last round of few tiles, e.g.
  * M 6144, N 3072, K 15360): those tiles' K ranges are summed in fp32 by a
- * second kernel, in a fixed order. Returns SELAS_EUNSUPPORTED
+ * second kernel, in a fixed order, from fp32 partial tiles kept in `workspace`
+ * (device memory of workspace_bytes >= selas_linear_workspace_bytes for this
+ * shape, 16-byte aligned, not read or written by anything else until the
+ * launch has run; NULL and 0 where that size is 0, otherwise SELAS_EINVAL).
+ * Whether and how a launch splits depends on M, N, K and the CU count only.
+ * Returns SELAS_EUNSUPPORTED
  * when the shape or layout is outside the fused kernels (blocksize != 64,
  * K % 64 != 0, misaligned rows, dtype other than bf16); the caller then
  * decodes with selas_nf4_dequant and uses a library GEMM.
@@ -124,7 +131,8 @@ int selas_int8_row_encode(const float *w, int64_t rows, int64_t cols, int8_t *q,
  */
 int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uint8_t *packed,
                      const float *absmax, int64_t blocksize, const float code[16], int64_t N,
-                     const void *bias, void *y, int64_t ldy, int dtype, void *stream);
+                     const void *bias, void *y, int64_t ldy, int dtype, void *workspace, int64_t workspace_bytes,
+                     void *stream);
 
 /* At most this many linears per selas_nf4_linear_batched call. */
 #define SELAS_MAX_BATCHED_LINEARS 4
@@ -155,7 +163,12 @@ typedef struct selas_nf4_gemm_problem {
  * x, weight, bias and y; all M > 32) in one launch of the tiled GEMM: the
  * tiles of all problems share the GPU, so a small problem fills the CUs a
  * large one leaves idle in its last round. Each y has the bits
- * selas_nf4_linear gives for that problem alone. Returns SELAS_EUNSUPPORTED,
+ * selas_nf4_linear gives for that problem alone, except in tiles that the
+ * batch's launch splits over K (the plan, like the workspace it needs, depends
+ * on all the problems' shapes: e.g. 4096- and 2048-token problems of
+ * K 12288 together leave a last round of few tiles that neither leaves alone).
+ * workspace / workspace_bytes as for selas_nf4_linear, sized by
+ * selas_linear_workspace_bytes over the same problems. Returns SELAS_EUNSUPPORTED,
  * launching nothing, when any problem is outside the tiled GEMM (M <= 32 or
  * any reason selas_nf4_linear would give); the caller then runs them one by one.
  * No counterpart in the reference: it replaces consecutive UnitView.linear
@@ -163,7 +176,22 @@ typedef struct selas_nf4_gemm_problem {
  * double block (selas/models/flux.py:300-324).
  */
 int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
-                             const float code[16], int dtype, void *stream);
+                             const float code[16], int dtype, void *workspace, int64_t workspace_bytes,
+                             void *stream);
+
+/*
+ * Bytes of device workspace that selas_nf4_linear (count 1) or
+ * selas_nf4_linear_batched (codec SELAS_CODEC_NF4), or their int8_row twins
+ * (SELAS_CODEC_INT8_ROW), need for these problems on the current device:
+ * 0 unless the launch splits its last round of tiles over K, then
+ * split tiles x K ranges x 256 KiB (at most the CU count x 256 KiB, 64 MiB on
+ * MI355X). Reads only M, K and N of each problem (the other fields may be
+ * NULL); problems with M = 0 are skipped, and M <= 32 gives 0 (skinny kernels).
+ * No counterpart in the reference: selas's decode-then-F.linear needs no
+ * scratch beyond the decoded weight (selas/store.py:289-293).
+ */
+int selas_linear_workspace_bytes(const selas_nf4_gemm_problem *problems, int64_t count, int codec,
+                                 int64_t *bytes);
 
 /*
  * Quantized linear forward y = x W^T + bias with W an int8_row [N, K] weight
@@ -174,21 +202,26 @@ int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t cou
  * runs a skinny kernel (for K = 1024, 2048, 3072 the streaming kernel of
  * selas_int8_row_linear_grouped) that multiplies x by q exactly and scales the fp32 row
  * sums by bf16(scale): it agrees with the decoded-weight product to the bf16
- * rounding of the decoded weight. Returns SELAS_EUNSUPPORTED for K % 64 != 0,
+ * rounding of the decoded weight. workspace / workspace_bytes as for
+ * selas_nf4_linear (selas_linear_workspace_bytes with SELAS_CODEC_INT8_ROW).
+ * Returns SELAS_EUNSUPPORTED for K % 64 != 0,
  * misaligned rows or a dtype other than bf16 (the caller then decodes with
  * selas_int8_row_dequant and uses a library GEMM).
  * Replaces UnitView.linear for int8_row weights (selas/store.py:289-293):
  * decode (codecs.py:273-277) followed by F.linear.
  */
 int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const int8_t *q, const float *scale,
-                          int64_t N, const void *bias, void *y, int64_t ldy, int dtype, void *stream);
+                          int64_t N, const void *bias, void *y, int64_t ldy, int dtype, void *workspace,
+                          int64_t workspace_bytes, void *stream);
 
 /*
  * selas_nf4_linear_batched for int8_row weights: in each problem `packed`
- * holds q and `absmax` the row scales; gelu_cols and y2 as there.
+ * holds q and `absmax` the row scales; gelu_cols, y2 and the workspace as
+ * there (selas_linear_workspace_bytes with SELAS_CODEC_INT8_ROW).
  * No counterpart in the reference (see selas_nf4_linear_batched).
  */
-int selas_int8_row_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int dtype, void *stream);
+int selas_int8_row_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int dtype, void *workspace,
+                                  int64_t workspace_bytes, void *stream);
 
 
 /*
@@ -222,19 +255,25 @@ int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx, c
 
 /* At most this many weights per selas_nf4_linear_grouped_static call. */
 #define SELAS_STATIC_MAX_WEIGHTS 1023
+/* At most this many streams per GPU call selas_nf4_linear_grouped_static. */
+#define SELAS_STATIC_MAX_STREAMS 8
 
 /*
  * selas_nf4_linear_grouped that allocates nothing and needs no device memory of
  * the caller's beyond x, the weights, biases and outputs: `descs` is an array
  * of `count` descriptors in HOST memory (read during the call only), and the
- * sum of their n is computed here. The library stages the descriptors in a
- * device table of its own, SELAS_STATIC_MAX_WEIGHTS * 48 bytes (49,104 bytes)
- * per GPU, held until the process ends; count above SELAS_STATIC_MAX_WEIGHTS
- * is rejected with SELAS_EINVAL. Every call on a GPU rewrites that table before
- * its kernels read it, so calls on one stream are ordered, but calls that
- * overlap on one GPU (on different streams, or from threads that do not
- * order them) race on it. Each output has the bits selas_nf4_linear_grouped
- * (and selas_nf4_linear) gives for that weight.
+ * sum of their n is computed here. The library stages the descriptors in
+ * device tables of its own: SELAS_STATIC_MAX_STREAMS tables of
+ * SELAS_STATIC_MAX_WEIGHTS * 48 bytes (392,832 bytes in all) per GPU, held until
+ * the process ends. Each stream that calls on a GPU gets its own table, at its
+ * first call; a call from a further stream returns SELAS_EUNSUPPORTED, and
+ * count above SELAS_STATIC_MAX_WEIGHTS is rejected with SELAS_EINVAL. A call
+ * rewrites its stream's table before its kernels read it, and enqueues both
+ * under that table's lock: calls on one stream are ordered (also from several
+ * host threads), and calls on different streams use different tables. A
+ * stream handle that is destroyed and handed out again keeps the old table, so
+ * the destroyed stream's calls must have finished. Each output has the bits
+ * selas_nf4_linear_grouped (and selas_nf4_linear) gives for that weight.
  * No counterpart in the reference. It is for callers that cannot allocate
  * device memory: code under HIP graph capture, serving loops with a fixed
  * memory budget, harnesses that forbid hipMalloc.

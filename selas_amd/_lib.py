@@ -14,10 +14,11 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libselas_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
+CODEC_NF4, CODEC_INT8_ROW = 0, 1
 
 DTYPE_CODES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -27,14 +28,15 @@ _F16x = ctypes.POINTER(ctypes.c_float)
 SIGNATURES: dict[str, list] = {
     "selas_nf4_dequant": [_P, _P, _I64, _I64, _F16x, _P, _INT, _P],
     "selas_nf4_encode": [_P, _I64, _I64, _F16x, _P, _P, _P],
-    "selas_nf4_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _F16x, _I64, _P, _P, _I64, _INT, _P],
+    "selas_nf4_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _F16x, _I64, _P, _P, _I64, _INT, _P, _I64, _P],
     "selas_nf4_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F16x, _INT, _P],
-    "selas_nf4_linear_batched": [_P, _I64, _I64, _F16x, _INT, _P],
+    "selas_nf4_linear_batched": [_P, _I64, _I64, _F16x, _INT, _P, _I64, _P],
+    "selas_linear_workspace_bytes": [_P, _I64, _INT, ctypes.POINTER(ctypes.c_int64)],
     "selas_nf4_linear_grouped_static": [_P, _I64, _I64, _I64, _P, _I64, _I64, _F16x, _INT, _P],
     "selas_int8_row_dequant": [_P, _P, _I64, _I64, _P, _INT, _P],
     "selas_int8_row_encode": [_P, _I64, _I64, _P, _P, _P],
-    "selas_int8_row_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _INT, _P],
-    "selas_int8_row_linear_batched": [_P, _I64, _INT, _P],
+    "selas_int8_row_linear": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _INT, _P, _I64, _P],
+    "selas_int8_row_linear_batched": [_P, _I64, _INT, _P, _I64, _P],
     "selas_int8_row_linear_grouped": [_P, _I64, _I64, _I64, _P, _I64, _I64, _INT, _P],
     "selas_mod_in": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _INT, _P],
     "selas_gated_add": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _INT, _I64, _I64, _INT, _P, _P],
@@ -67,6 +69,7 @@ class GemvDesc(ctypes.Structure):
 
 
 STATIC_MAX_WEIGHTS = 1023
+STATIC_MAX_STREAMS = 8
 
 
 class Unsupported(NotImplementedError):
@@ -118,6 +121,35 @@ def call(name: str, *args) -> None:
     if rc == EUNSUPPORTED:
         raise Unsupported(msg)
     raise HipError(msg)
+
+
+_ws_sizes: dict[tuple, int] = {}
+
+
+def workspace_bytes(codec: int, shapes, device: torch.device) -> int:
+    """Bytes of scratch a tiled linear launch over problems of these (M, K, N) shapes needs on ``device``
+    (selas_linear_workspace_bytes; 0 for most shapes). The answer depends on the shapes and the GPU's CU
+    count only, so it is kept per (device, codec, shapes)."""
+    key = (device.index, codec, tuple(shapes))
+    n = _ws_sizes.get(key)
+    if n is None:
+        arr = (GemmProblem * max(len(shapes), 1))()
+        for i, (m, k, nn) in enumerate(shapes):
+            arr[i].M, arr[i].K, arr[i].N = m, k, nn
+        out = ctypes.c_int64(0)
+        with torch.cuda.device(device):
+            call("selas_linear_workspace_bytes", ctypes.addressof(arr), len(shapes), codec, ctypes.byref(out))
+        n = _ws_sizes[key] = int(out.value)
+    return n
+
+
+def workspace(codec: int, shapes, device: torch.device) -> tuple[torch.Tensor | None, int]:
+    """(scratch tensor or None, its size in bytes) for a tiled linear launch: allocated from torch's caching
+    allocator on the current stream, per call, so stream-ordered reuse keeps it private to the launch."""
+    n = workspace_bytes(codec, shapes, device)
+    if n == 0:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=device), n
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -33,4 +33,4 @@ int check_launch(const char *what) {
 
 extern "C" const char *selas_last_error(void) { return g_msg; }
 
-extern "C" int selas_abi_version(void) { return 5; }
+extern "C" int selas_abi_version(void) { return 6; }

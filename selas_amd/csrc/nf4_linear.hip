@@ -26,6 +26,7 @@
 // load of packed codes feeds a lane for a whole 64-block. The 32x32 fp32
 // result has, in lane l, column l%32 and rows 8*(r/4) + 4*h + r%4, r = 0..15.
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -893,14 +894,24 @@ __global__ __launch_bounds__(64 * NW, 1) void int8_gemv_stream(
   finish((u_end - 1 - u_begin) & (L::kRedBufs - 1), d_prev, row_prev, bias_prev, scale_prev);
 }
 
+// The current device's CU count (queried once per device).
 int cu_count() {
-  static int n = [] {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    return v;
-  }();
-  return n;
+  constexpr int kDevices = 64;
+  static std::atomic<int> counts[kDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  const int slot = dev >= 0 && dev < kDevices ? dev : 0;
+  int v = counts[slot].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) {
+    (void)hipGetLastError();
+    v = 256;
+  }
+  counts[slot].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 // True when the streaming kernel covers K.
@@ -1685,48 +1696,24 @@ __global__ __launch_bounds__(256) void gemm_tail_sum(GemmBatch batch) {
   }
 }
 
-// fp32 partial tiles of split launches: one buffer of `bytes` per (device,
-// stream), allocated at the first split launch and kept until the process ends.
-// Launches on one stream run in order and share it; launches on different
-// streams get different buffers, for at most kMaxSplitStreams streams per
-// device (a caller that makes a stream per request does not grow memory
-// without bound). nullptr when the allocation fails or the streams are used up
-// (the caller then launches without a split).
-constexpr int kMaxSplitStreams = 8;
-float *split_workspace(hipStream_t s, size_t bytes) {
-  struct Entry {
-    int dev;
-    hipStream_t s;
-    void *p;
-  };
-  static std::mutex mu;
-  static std::vector<Entry> entries;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> g(mu);
-  int on_dev = 0;
-  for (const Entry &e : entries) {
-    if (e.dev == dev && e.s == s) return static_cast<float *>(e.p);
-    on_dev += e.dev == dev;
-  }
-  if (on_dev >= kMaxSplitStreams) return nullptr;
-  void *p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  entries.push_back(Entry{dev, s, p});
-  return static_cast<float *>(p);
-}
+// fp32 partial tiles of a split launch: split * tail tiles of 256 x 256 floats.
+constexpr int64_t kSplitTileBytes = 256 * 256 * 4;
+
+// How a tiled batch runs: tile height 32 * mb, and whether the last round's
+// `tail` tiles run as `split` K ranges each. Chosen from the shapes and the
+// GPU's CU count only, so a call's bits never depend on anything else.
+struct GemmPlan {
+  int mb = 8;
+  int split = 1;
+  int64_t tail = 0;
+  int64_t workspace_bytes() const { return split > 1 ? tail * split * kSplitTileBytes : 0; }
+};
 
 // `batch.p[0..count)` filled except tiles_n / tile0, which are set here. With
-// split > 1 the last round's tiles (tiles % CUs of them) run as `split` K ranges
-// each, when a workspace for their partial tiles is available.
+// split > 1 the last round's tiles (tiles % CUs of them, MB = 8) run as `split`
+// K ranges each, their fp32 partial tiles in `part`.
 template <int MB, int CB, int STAGES, int NW>
-void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4, int split = 1) {
+void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc, int split, float *part) {
   int64_t tiles = 0;
   for (int i = 0; i < batch.count; ++i) {
     GemmProblem &p = batch.p[i];
@@ -1736,17 +1723,11 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
     tiles += tiles_m * tiles_n;
   }
   constexpr int64_t kTileBytes = 32 * MB * 32 * CB * NW * 4;
-  const int64_t tail = tiles % cu_count();
+  static_assert(MB != 8 || kTileBytes == kSplitTileBytes, "split tile size");
   batch.tiles = static_cast<int>(tiles);
-  batch.tail = 0;
-  batch.split = 1;
-  batch.part = nullptr;
-  if (MB == 8 && split > 1 && split <= kMaxSplit && tail > 0 && tail * split <= cu_count() && tiles > tail)
-    batch.part = split_workspace(s, static_cast<size_t>(cu_count()) * (256 * 256 * 4));  // the largest tile
-  if (batch.part) {
-    batch.tail = static_cast<int>(tail);
-    batch.split = split;
-  }
+  batch.tail = MB == 8 && split > 1 ? static_cast<int>(tiles % cu_count()) : 0;
+  batch.split = batch.tail ? split : 1;
+  batch.part = batch.tail ? part : nullptr;
   batch.per_xcd = static_cast<int>(cdiv(tiles - batch.tail, 8));
   batch.dp_blocks = batch.per_xcd * 8;
   batch.tail_per_xcd = static_cast<int>(cdiv(static_cast<int64_t>(batch.tail) * batch.split, 8));
@@ -1772,7 +1753,7 @@ void launch_gemm(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = W
 // N 3072) takes 252 224-row ones, the same single round.
 // 128 x 512 tiles of 8 waves (128 x 64 each, two waves per SIMD) measured 15-25 %
 // slower: each decoded weight fragment then serves 4 MFMAs instead of 8.
-void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc = WCodec::kNF4) {
+GemmPlan plan_gemm(const GemmBatch &batch, WCodec wc) {
   auto cost = [&](int mb, double tile_time) {
     int64_t tiles = 0;
     for (int i = 0; i < batch.count; ++i) tiles += cdiv(batch.p[i].M, 32 * mb) * cdiv(batch.p[i].N, 256);
@@ -1796,7 +1777,7 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
   // and read back) and the summing launch ~3 us. Taken when the estimate beats
   // the best single height by 5 % (long K: 4 x 1536 tokens x 3072 x 15360, 288
   // tiles, 580 us with 192-row tiles).
-  int split = 0;
+  GemmPlan plan;
   bool one_k = true;
   for (int i = 1; i < batch.count; ++i) one_k = one_k && batch.p[i].K == batch.p[0].K;
   if (one_k && t8 > cu && t8 % cu) {
@@ -1804,6 +1785,7 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
     const double tt = 14.0 + 1.48 * static_cast<double>(kb);
     const double best = std::min(c8, std::min(c7, c6)) * tt;
     double est = 0.0;
+    int split = 0;
     for (int S = 2; S <= kMaxSplit && tail * S <= cu && kb >= 3 * S; ++S) {
       const double e = static_cast<double>(t8 / cu) * tt + 14.0 + 1.48 * static_cast<double>(kb) / S + 3.0 +
                        0.1 * static_cast<double>(tail * S);
@@ -1812,13 +1794,38 @@ void launch_gemm_default(GemmBatch &batch, const Code16 &c, hipStream_t s, WCode
         split = S;
       }
     }
-    if (split && !(est < 0.95 * best)) split = 0;
+    if (split && est < 0.95 * best) {
+      plan.split = split;
+      plan.tail = tail;
+      return plan;
+    }
   }
-  if (split) launch_gemm<8, 2, 3, 4>(batch, c, s, wc, split);
-  else if (wc == WCodec::kNF4 && t8 <= cu && 4 * t8 >= 3 * cu) launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
-  else if (c6 < 0.98 * c7 && c6 < 0.98 * c8) launch_gemm<6, 2, 3, 4>(batch, c, s, wc);
-  else if (c7 < 0.98 * c8) launch_gemm<7, 2, 3, 4>(batch, c, s, wc);
-  else launch_gemm<8, 2, 3, 4>(batch, c, s, wc);
+  if (wc == WCodec::kNF4 && t8 <= cu && 4 * t8 >= 3 * cu) plan.mb = 8;
+  else if (c6 < 0.98 * c7 && c6 < 0.98 * c8) plan.mb = 6;
+  else if (c7 < 0.98 * c8) plan.mb = 7;
+  return plan;
+}
+
+void launch_plan(GemmBatch &batch, const GemmPlan &plan, const Code16 &c, hipStream_t s, WCodec wc, float *part) {
+  switch (plan.mb) {
+    case 6: launch_gemm<6, 2, 3, 4>(batch, c, s, wc, 1, nullptr); break;
+    case 7: launch_gemm<7, 2, 3, 4>(batch, c, s, wc, 1, nullptr); break;
+    default: launch_gemm<8, 2, 3, 4>(batch, c, s, wc, plan.split, part); break;
+  }
+}
+
+// Plans a batch and checks the caller's workspace against what the plan needs.
+int plan_and_launch(const char *what, GemmBatch &batch, const Code16 &c, hipStream_t s, WCodec wc, void *workspace,
+                    int64_t workspace_bytes) {
+  const GemmPlan plan = plan_gemm(batch, wc);
+  const int64_t need = plan.workspace_bytes();
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
+    return set_error(SELAS_EINVAL,
+                     "%s: this launch splits its last round of tiles over K and needs a 16-byte aligned workspace of "
+                     "%lld bytes (selas_linear_workspace_bytes); got %lld bytes at %p",
+                     what, (long long)need, (long long)workspace_bytes, workspace);
+  launch_plan(batch, plan, c, s, wc, static_cast<float *>(workspace));
+  return check_launch(what);
 }
 
 }  // namespace
@@ -1866,7 +1873,8 @@ int check_linear(const char *what, const void *x, int64_t M, int64_t K, int64_t 
 
 extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const uint8_t *packed,
                                 const float *absmax, int64_t blocksize, const float code[16], int64_t N,
-                                const void *bias, void *y, int64_t ldy, int dtype, void *stream) {
+                                const void *bias, void *y, int64_t ldy, int dtype, void *workspace,
+                                int64_t workspace_bytes, void *stream) {
   if (int e = check_linear("nf4_linear", x, M, K, ldx, packed, absmax, blocksize, code, N, bias, y, ldy, dtype))
     return e;
   if (M == 0) return ok();
@@ -1891,18 +1899,17 @@ extern "C" int selas_nf4_linear(const void *x, int64_t M, int64_t K, int64_t ldx
   batch.count = 1;
   batch.p[0] = GemmProblem{xb, packed, absmax, bb, yb, nullptr, ldx, ldy, 0, static_cast<int>(M),
                            static_cast<int>(K), static_cast<int>(N), static_cast<int>(N), 0, 0};
-  launch_gemm_default(batch, c, s);
-  return check_launch("nf4_linear (gemm)");
+  return plan_and_launch("nf4_linear (gemm)", batch, c, s, WCodec::kNF4, workspace, workspace_bytes);
 }
 
 namespace {
-int linear_batched(const char *what, WCodec wc, const selas_nf4_gemm_problem *problems, int64_t count,
-                   int64_t blocksize, const float *code, int dtype, void *stream) {
+// Validates the problems of a batched call into `batch` (M = 0 problems left out).
+int fill_batch(const char *what, WCodec wc, const selas_nf4_gemm_problem *problems, int64_t count,
+               int64_t blocksize, const float *code, int dtype, GemmBatch &batch) {
   static_assert(kGemmMaxProblems == SELAS_MAX_BATCHED_LINEARS, "batch size");
   if (count < 0 || count > kGemmMaxProblems)
     return set_error(SELAS_EINVAL, "%s: count %lld outside [0, %d]", what, (long long)count, kGemmMaxProblems);
   if (count > 0 && !problems) return set_error(SELAS_EINVAL, "%s: null problems", what);
-  GemmBatch batch{};
   for (int64_t i = 0; i < count; ++i) {
     const selas_nf4_gemm_problem &q = problems[i];
     const int64_t gc = q.gelu_cols;
@@ -1934,28 +1941,66 @@ int linear_batched(const char *what, WCodec wc, const selas_nf4_gemm_problem *pr
                                          static_cast<int>(q.M), static_cast<int>(q.K), static_cast<int>(q.N),
                                          static_cast<int>(q.N - gc), 0, 0};
   }
+  return SELAS_OK;
+}
+
+int linear_batched(const char *what, WCodec wc, const selas_nf4_gemm_problem *problems, int64_t count,
+                   int64_t blocksize, const float *code, int dtype, void *workspace, int64_t workspace_bytes,
+                   void *stream) {
+  GemmBatch batch{};
+  if (int e = fill_batch(what, wc, problems, count, blocksize, code, dtype, batch)) return e;
   if (batch.count == 0) return ok();
   Code16 c{};
   if (wc == WCodec::kNF4)
     for (int i = 0; i < 16; ++i) c.v[i] = code[i];
-  launch_gemm_default(batch, c, static_cast<hipStream_t>(stream), wc);
-  return check_launch(what);
+  return plan_and_launch(what, batch, c, static_cast<hipStream_t>(stream), wc, workspace, workspace_bytes);
 }
 }  // namespace
 
 extern "C" int selas_nf4_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int64_t blocksize,
-                                        const float code[16], int dtype, void *stream) {
-  return linear_batched("nf4_linear_batched", WCodec::kNF4, problems, count, blocksize, code, dtype, stream);
+                                        const float code[16], int dtype, void *workspace, int64_t workspace_bytes,
+                                        void *stream) {
+  return linear_batched("nf4_linear_batched", WCodec::kNF4, problems, count, blocksize, code, dtype, workspace,
+                        workspace_bytes, stream);
 }
 
 extern "C" int selas_int8_row_linear_batched(const selas_nf4_gemm_problem *problems, int64_t count, int dtype,
-                                             void *stream) {
-  return linear_batched("int8_row_linear_batched", WCodec::kInt8Row, problems, count, 0, nullptr, dtype, stream);
+                                             void *workspace, int64_t workspace_bytes, void *stream) {
+  return linear_batched("int8_row_linear_batched", WCodec::kInt8Row, problems, count, 0, nullptr, dtype, workspace,
+                        workspace_bytes, stream);
+}
+
+extern "C" int selas_linear_workspace_bytes(const selas_nf4_gemm_problem *problems, int64_t count, int codec,
+                                            int64_t *bytes) {
+  if (!bytes) return set_error(SELAS_EINVAL, "linear_workspace_bytes: null result pointer");
+  *bytes = 0;
+  if (codec != SELAS_CODEC_NF4 && codec != SELAS_CODEC_INT8_ROW)
+    return set_error(SELAS_EINVAL, "linear_workspace_bytes: unknown codec %d", codec);
+  if (count < 0 || count > kGemmMaxProblems)
+    return set_error(SELAS_EINVAL, "linear_workspace_bytes: count %lld outside [0, %d]", (long long)count,
+                     kGemmMaxProblems);
+  if (count > 0 && !problems) return set_error(SELAS_EINVAL, "linear_workspace_bytes: null problems");
+  GemmBatch batch{};
+  for (int64_t i = 0; i < count; ++i) {
+    const selas_nf4_gemm_problem &q = problems[i];
+    if (q.M < 0 || q.K <= 0 || q.N <= 0 || q.M > INT32_MAX || q.K > INT32_MAX || q.N > INT32_MAX)
+      return set_error(SELAS_EINVAL, "linear_workspace_bytes: bad shape M=%lld K=%lld N=%lld", (long long)q.M,
+                       (long long)q.K, (long long)q.N);
+    if (q.M == 0) continue;
+    if (q.M <= 32) return ok();  // the skinny kernels, or a batch that runs one by one: no workspace
+    GemmProblem &p = batch.p[batch.count++];
+    p.M = static_cast<int>(q.M);
+    p.K = static_cast<int>(q.K);
+    p.N = static_cast<int>(q.N);
+  }
+  if (batch.count == 0) return ok();
+  *bytes = plan_gemm(batch, codec == SELAS_CODEC_NF4 ? WCodec::kNF4 : WCodec::kInt8Row).workspace_bytes();
+  return ok();
 }
 
 extern "C" int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_t ldx, const int8_t *q,
                                      const float *scale, int64_t N, const void *bias, void *y, int64_t ldy, int dtype,
-                                     void *stream) {
+                                     void *workspace, int64_t workspace_bytes, void *stream) {
   const uint8_t *qb = reinterpret_cast<const uint8_t *>(q);
   if (int e = check_linear("int8_row_linear", x, M, K, ldx, qb, scale, 0, nullptr, N, bias, y, ldy, dtype,
                            WCodec::kInt8Row))
@@ -1979,8 +2024,8 @@ extern "C" int selas_int8_row_linear(const void *x, int64_t M, int64_t K, int64_
   batch.count = 1;
   batch.p[0] = GemmProblem{xb, qb, scale, bb, yb, nullptr, ldx, ldy, 0, static_cast<int>(M),
                            static_cast<int>(K), static_cast<int>(N), static_cast<int>(N), 0, 0};
-  launch_gemm_default(batch, Code16{}, s, WCodec::kInt8Row);
-  return check_launch("int8_row_linear (gemm)");
+  return plan_and_launch("int8_row_linear (gemm)", batch, Code16{}, s, WCodec::kInt8Row, workspace,
+                         workspace_bytes);
 }
 
 extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int64_t ldx,
@@ -2038,23 +2083,29 @@ extern "C" int selas_int8_row_linear_grouped(const void *x, int64_t M, int64_t K
 // ------------------------------------------------ grouped skinny GEMM without caller memory
 //
 // selas_nf4_linear_grouped reads its weight descriptors from a device array the
-// caller allocates. This variant takes them in host memory and stages them in a
-// descriptor table of the library's own: `scratch`, a device array of the code
-// object (one copy per GPU, held until the process ends). Its device address
-// comes from hipGetSymbolAddress once per device, on the first call there, and
-// only that address is passed to kernels: the array's name in host code is a
-// host-side stand-in, not a device address. The descriptors reach it as kernel
-// arguments of a small copy kernel (kStageDescs per launch), so no copy from
-// host memory and no allocation is made. Every call on a GPU rewrites the
-// table before reading it; calls that overlap on one GPU (different streams)
-// race on it.
+// caller allocates. This variant takes them in host memory and stages them in
+// descriptor tables of the library's own: `scratch`, a device array of the code
+// object (one copy per GPU, held until the process ends) that holds
+// kStaticStreams tables. Its device address comes from hipGetSymbolAddress once
+// per device, on the first call there, and only that address is passed to
+// kernels: the array's name in host code is a host-side stand-in, not a device
+// address. Each (device, stream) pair that calls gets a table of its own, up to
+// kStaticStreams per device; further streams are refused (SELAS_EUNSUPPORTED),
+// so two streams never share a table. The descriptors reach the table as
+// kernel arguments of a small copy kernel (kStageDescs per launch), so no copy
+// from host memory and no allocation is made. A call's copies and its GEMM are
+// enqueued under the table's lock, so host threads that share a stream cannot
+// interleave them; the stream orders one call's GEMM before the next call's
+// copies.
 namespace {
-constexpr int kStaticDescs = kSgMaxDescs;  // 1023 descriptors, 49,104 bytes
+constexpr int kStaticDescs = kSgMaxDescs;  // 1023 descriptors, 49,104 bytes per table
+constexpr int kStaticStreams = 8;          // tables per GPU (392,832 bytes)
 constexpr int kStageDescs = 64;            // descriptors per copy launch (3,072 bytes of arguments)
 constexpr int kMaxDevices = 64;
 static_assert(kStaticDescs == SELAS_STATIC_MAX_WEIGHTS, "scratch size");
+static_assert(kStaticStreams == SELAS_STATIC_MAX_STREAMS, "scratch tables");
 
-__device__ __align__(256) GemvDesc scratch[kStaticDescs];
+__device__ __align__(256) GemvDesc scratch[kStaticStreams * kStaticDescs];
 
 struct DescChunk {
   GemvDesc d[kStageDescs];
@@ -2067,26 +2118,44 @@ __global__ __launch_bounds__(kStageDescs) void stage_descs(DescChunk c, GemvDesc
   if (i < c.count) dst[c.first + i] = c.d[i];
 }
 
+struct StaticDevice {
+  GemvDesc *base = nullptr;  // device address of `scratch` on this device
+  hipStream_t streams[kStaticStreams] = {};
+  int used = 0;
+  std::mutex table_mu[kStaticStreams];
+};
 std::mutex scratch_mu;
-GemvDesc *scratch_ptr[kMaxDevices];
+StaticDevice static_devices[kMaxDevices];
 
-// The device address of `scratch` on the current device (resolved once per device).
-int scratch_table(GemvDesc **out) {
+// The table of (current device, stream) and its lock; the device's scratch
+// address is resolved on its first call.
+int scratch_table(hipStream_t s, GemvDesc **out, std::mutex **lock) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return set_error(SELAS_EHIP, "nf4_linear_grouped_static: hipGetDevice: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= kMaxDevices)
     return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: device %d beyond %d", dev, kMaxDevices);
-  std::lock_guard<std::mutex> lock(scratch_mu);
-  if (!scratch_ptr[dev]) {
+  std::lock_guard<std::mutex> g(scratch_mu);
+  StaticDevice &d = static_devices[dev];
+  if (!d.base) {
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return set_error(SELAS_EHIP, "nf4_linear_grouped_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
                        hipGetErrorString(e));
-    scratch_ptr[dev] = static_cast<GemvDesc *>(p);
+    d.base = static_cast<GemvDesc *>(p);
   }
-  *out = scratch_ptr[dev];
+  int slot = 0;
+  while (slot < d.used && d.streams[slot] != s) ++slot;
+  if (slot == d.used) {
+    if (d.used == kStaticStreams)
+      return set_error(SELAS_EUNSUPPORTED,
+                       "nf4_linear_grouped_static: %d streams on device %d already hold its descriptor tables",
+                       kStaticStreams, dev);
+    d.streams[d.used++] = s;
+  }
+  *out = d.base + static_cast<int64_t>(slot) * kStaticDescs;
+  *lock = &d.table_mu[slot];
   return SELAS_OK;
 }
 }  // namespace
@@ -2123,9 +2192,11 @@ extern "C" int selas_nf4_linear_grouped_static(const void *x, int64_t M, int64_t
                        (long long)i);
     total_n += d.n;
   }
-  GemvDesc *table = nullptr;
-  if (int e = scratch_table(&table)) return e;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  GemvDesc *table = nullptr;
+  std::mutex *table_mu = nullptr;
+  if (int e = scratch_table(s, &table, &table_mu)) return e;
+  std::lock_guard<std::mutex> g(*table_mu);
   for (int64_t first = 0; first < count; first += kStageDescs) {
     DescChunk chunk{};
     chunk.first = static_cast<int>(first);

@@ -78,10 +78,11 @@ def nf4_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor, bloc
     try:
         if x.dtype not in _lib.DTYPE_CODES:
             raise _lib.Unsupported(f"dtype {x.dtype}")
+        ws, ws_bytes = _lib.workspace(_lib.CODEC_NF4, ((m, k, n),), dev) if m > 32 else (None, 0)
         with torch.cuda.device(dev):
             _lib.call("selas_nf4_linear", x2.data_ptr(), m, k, x2.stride(0), packed.data_ptr(), absmax.data_ptr(),
                       int(blocksize), _lib.code_array(code), n, _lib.ptr(bias), y.data_ptr(), n,
-                      _lib.dtype_code(x.dtype), _lib.stream(dev))
+                      _lib.dtype_code(x.dtype), _lib.ptr(ws), ws_bytes, _lib.stream(dev))
         return y
     except _lib.Unsupported:
         w = nf4_dequant(packed, absmax, blocksize, code, (n, k), x.dtype)
@@ -108,9 +109,11 @@ def int8_row_linear(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, shape
     try:
         if x.dtype not in _lib.DTYPE_CODES:
             raise _lib.Unsupported(f"dtype {x.dtype}")
+        ws, ws_bytes = _lib.workspace(_lib.CODEC_INT8_ROW, ((m, k, n),), dev) if m > 32 else (None, 0)
         with torch.cuda.device(dev):
             _lib.call("selas_int8_row_linear", x2.data_ptr(), m, k, x2.stride(0), q.data_ptr(), scale.data_ptr(), n,
-                      _lib.ptr(bias), y.data_ptr(), n, _lib.dtype_code(x.dtype), _lib.stream(dev))
+                      _lib.ptr(bias), y.data_ptr(), n, _lib.dtype_code(x.dtype), _lib.ptr(ws), ws_bytes,
+                      _lib.stream(dev))
         return y
     except _lib.Unsupported:
         return F.linear(x, int8_row_dequant(q, scale, x.dtype).view(n, k), bias)
@@ -126,12 +129,17 @@ def _single(codec: str, p) -> torch.Tensor:
 
 
 def _launch_batched(codec: str, arr, count: int, code, dev) -> None:
+    """One tiled launch over ``arr[:count]``, with the split-tail scratch (if its plan has one) allocated here."""
+    shapes = tuple((arr[i].M, arr[i].K, arr[i].N) for i in range(count) if arr[i].M > 0)
+    cc = _lib.CODEC_NF4 if codec == "nf4" else _lib.CODEC_INT8_ROW
+    ws, ws_bytes = _lib.workspace(cc, shapes, dev) if shapes else (None, 0)
     with torch.cuda.device(dev):
         if codec == "nf4":
             _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), count, 64, _lib.code_array(code), _lib.BF16,
-                      _lib.stream(dev))
+                      _lib.ptr(ws), ws_bytes, _lib.stream(dev))
         else:
-            _lib.call("selas_int8_row_linear_batched", ctypes.addressof(arr), count, _lib.BF16, _lib.stream(dev))
+            _lib.call("selas_int8_row_linear_batched", ctypes.addressof(arr), count, _lib.BF16, _lib.ptr(ws), ws_bytes,
+                      _lib.stream(dev))
 
 
 def _batch_eligible(codec: str, problems):
@@ -158,8 +166,10 @@ def nf4_linear_batched(problems) -> list[torch.Tensor]:
     ``nf4_linear``, with independent inputs (e.g. the image and text streams of a double
     block, selas/models/flux.py:300-324). The tiles of all problems share the GPU, so a
     small problem runs in the CUs a large one leaves idle. Each result has the bits of
-    its own ``nf4_linear`` call; when any problem is outside the tiled GEMM (rows <= 32,
-    unsupported shapes) they run one by one.
+    its own ``nf4_linear`` call, except in tiles that the batch's launch splits over K
+    (long K with a last round of few tiles, decided from all the problems' shapes),
+    whose fp32 partial sums are added in another order; when any problem is outside the
+    tiled GEMM (rows <= 32, unsupported shapes) they run one by one.
     """
     return _batched("nf4", list(problems))
 

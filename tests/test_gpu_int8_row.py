@@ -187,7 +187,8 @@ def test_unsupported_shape_falls_back_to_decode_and_library_gemm(dev):
         x = torch.randn(m, k, generator=seeded(14)).to(torch.bfloat16).to(dev)
         with pytest.raises(_lib.Unsupported):
             _lib.call("selas_int8_row_linear", x.data_ptr(), m, k, k, q.data_ptr(), s.data_ptr(), n, None,
-                      torch.empty(m, n, dtype=torch.bfloat16, device=dev).data_ptr(), n, _lib.BF16, _lib.stream(dev))
+                      torch.empty(m, n, dtype=torch.bfloat16, device=dev).data_ptr(), n, _lib.BF16, None, 0,
+                      _lib.stream(dev))
         check_close(int8_row_linear(x, q, s, (n, k)), oracle_linear(x, w_ref))
 
 

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import nf4 as onf4
-from selas_amd import codecs
+from selas_amd import _lib, codecs
 from selas_amd.linear import UnitView, nf4_linear
 
 from .conftest import seeded
@@ -260,7 +260,7 @@ def test_bits_do_not_depend_on_concurrent_kernels(dev, m, n, k):
     # wait there counted loads that the compiler had deleted, and the last block's x tile could still be
     # in flight when it was read, which showed only when another kernel slowed the loads down (16384
     # rows: 256 tiles in one round). 16640 rows also split the last round's 4 tiles over K, whose partial
-    # tiles live in one workspace per stream. 1536 x 12288 x 128 runs 192-row tiles with two blocks after
+    # tiles live in a workspace each call allocates. 1536 x 12288 x 128 runs 192-row tiles with two blocks after
     # the (empty) loop.
     p, a, _ = make_weight(n, k, 91, dev)
     xs = [torch.randn(m, k, generator=seeded(92 + i)).to(torch.bfloat16).to(dev) for i in range(2)]
@@ -285,10 +285,11 @@ def test_bits_do_not_depend_on_concurrent_kernels(dev, m, n, k):
 
 
 def test_split_launches_on_many_streams(dev):
-    # One split workspace per stream for up to 8 streams per device; launches on further streams run
-    # unsplit. Either way the whole tiles give the same bits and the split ones agree to the order of the
-    # fp32 sums (M = 16640, N = 1024, K = 2048: the last row slab is split on 256 CUs).
+    # The split plan and its workspace come from the shapes alone (the caller allocates the workspace per
+    # call), so every stream gives the same bits: 12 streams at once, with the default stream's result
+    # (M = 16640, N = 1024, K = 2048: the last row slab's 4 tiles run as 8 K ranges each on 256 CUs).
     m, n, k = 16640, 1024, 2048
+    assert _lib.workspace_bytes(_lib.CODEC_NF4, ((m, k, n),), dev) == 4 * 8 * 256 * 1024
     p, a, w_ref = make_weight(n, k, 101, dev)
     x = torch.randn(m, k, generator=seeded(102)).to(torch.bfloat16).to(dev)
     ref = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None)
@@ -300,11 +301,40 @@ def test_split_launches_on_many_streams(dev):
             outs.append(nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None))
     torch.cuda.synchronize()
     for y in outs:
-        assert torch.equal(y[:16384], ref[:16384])
-        d = (y[16384:].double() - ref[16384:].double()).norm() / ref[16384:].double().norm()
-        assert d.item() < 1e-4
+        assert torch.equal(y, ref)
+    # the split tiles sum K in another order than a launch of their rows alone (one round, unsplit)
+    alone = nf4_linear(x[16384:], p, a, 64, codecs.NF4_CODE, (n, k), None)
+    d = (ref[16384:].double() - alone.double()).norm() / alone.double().norm()
+    assert d.item() < 1e-4
     rows = torch.arange(16384, m, 8)
     check_close(outs[-1][rows], oracle_linear(x[rows], w_ref, None))
+
+
+def test_split_launch_in_a_captured_graph(dev):
+    # A split shape captured in a HIP graph (its workspace comes from the graph's memory pool) and replayed
+    # several times, with eager work between the replays: every replay gives the eager launch's bits.
+    m, n, k = 16640, 1024, 2048
+    p, a, _ = make_weight(n, k, 103, dev)
+    x = torch.randn(m, k, generator=seeded(104)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(n, generator=seeded(105)) * 0.02).to(torch.bfloat16).to(dev)
+    eager = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm the wrapper's caches outside capture
+        nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), b)
+    for i in range(4):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y, eager), i
+        other = nf4_linear(x[:4096], p, a, 64, codecs.NF4_CODE, (n, k), b)  # eager work between replays
+        torch.cuda.synchronize(dev)
+        assert torch.equal(other, eager[:4096])
 
 
 def test_tile_height_does_not_change_the_bits(dev):

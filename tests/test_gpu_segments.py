@@ -113,3 +113,57 @@ def test_gelu_and_attn_mlp(dev):
     close(g, S.gelu(h[..., :1000].float()))
     small = torch.randn(3, 7, generator=seeded(21)).to(BF)  # odd width: the scalar path
     close(K.gelu(small.to(dev)), S.gelu(small.float()))
+
+
+def test_unsupported_calls_fall_back_to_the_eager_segment(dev):
+    # Calls the kernels do not take run the eager segment on the GPU, with one warning per segment (as
+    # selas's compiled segments fall back to eager ones, flux.py:215-235): a width that is not a multiple
+    # of 4 (D = 1002), qkv rows 2 bytes off alignment, fp32 attn_mlp, a bf16 residual stream.
+    import warnings
+
+    from selas_amd import kernels
+
+    kernels._warned.clear()
+    b, l, d = 2, 9, 1002
+    x = torch.randn(b, l, d, generator=seeded(40))
+    y = torch.randn(b, l, d, generator=seeded(41)).to(BF)
+    _, (sh, sc, g) = mods(b, d, 3, 42)
+    with pytest.warns(RuntimeWarning, match="mod_in"):
+        out = K.mod_in(x.to(dev), sh.to(dev), sc.to(dev), BF)
+    close(out, S.mod_in(x, sh, sc, torch.float32))
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # once per segment: the second call is quiet
+        K.mod_in(x.to(dev), sh.to(dev), sc.to(dev), BF)
+    with pytest.warns(RuntimeWarning, match="gated_add_mod"):
+        xo, h = K.gated_add_mod(x.to(dev), g.to(dev), y.to(dev), sh.to(dev), sc.to(dev), BF, False)
+    rx, rh = S.gated_add_mod(x, g, y, sh, sc, torch.float32, False)
+    assert torch.allclose(xo.cpu(), rx, rtol=1e-5, atol=1e-5)
+    close(h, rh)
+    with pytest.warns(RuntimeWarning, match="gated_add"):
+        close(K.gated_add(x.to(dev), g.to(dev), y.to(dev), False), S.gated_add(x, g, y, False), 1e-5, 1e-5)
+    # qkv rows starting 2 bytes into a buffer
+    heads, dh, lq = 2, 64, 16
+    base = torch.randn(1, lq, 3 * heads * dh + 1, generator=seeded(43)).to(BF)
+    qkv = base[..., 1:]
+    qs, ks = 1 + 0.02 * torch.randn(dh, generator=seeded(44)), 1 + 0.02 * torch.randn(dh, generator=seeded(45))
+    cos, sin = S.rope_tables(torch.zeros(lq, 3), (16, 24, 24), 10000.0)
+    qkv_dev = base.to(dev)[..., 1:]  # sliced on the GPU: a copy of the view would be aligned again
+    assert qkv_dev.data_ptr() % 4 == 2
+    with pytest.warns(RuntimeWarning, match="qkv_single"):
+        q, k, v = K.qkv_single(qkv_dev, qs.to(dev), ks.to(dev), cos.to(dev), sin.to(dev), heads, BF)
+    rq, rk, rv = S.qkv_single(qkv, qs, ks, cos, sin, heads, BF)
+    close(q, rq)
+    close(k, rk)
+    assert torch.equal(v.cpu(), rv)
+    # attn_mlp in fp32
+    attn, mlp = torch.randn(1, 5, 64, generator=seeded(46)), torch.randn(1, 5, 96, generator=seeded(47))
+    with pytest.warns(RuntimeWarning, match="attn_mlp"):
+        o = K.attn_mlp(attn.to(dev), mlp.to(dev))
+    close(o, S.attn_mlp(attn, mlp), 1e-5, 1e-5)
+    # a bf16 residual stream (the kernels take fp32)
+    xb = torch.randn(1, 4, 256, generator=seeded(48)).to(BF)
+    _, (sh2, sc2, _) = mods(1, 256, 3, 49)
+    close(K.mod_in(xb.to(dev), sh2.to(dev), sc2.to(dev), BF), S.mod_in(xb, sh2, sc2, BF))
+    # argument errors are still errors
+    with pytest.raises(ValueError):
+        K.qkv_single(qkv_dev, qs[:5].to(dev), ks.to(dev), cos.to(dev), sin.to(dev), heads, BF)

@@ -236,38 +236,63 @@ def bench_modulations(dev, steps, warmup):
     flops = sum(2.0 * s * e.shape[0] * D for e in ws)
     tuples = [(e.parts["packed"], e.parts["absmax"], 64, codecs.NF4_CODE, e.shape, b) for e, b in zip(ws, bs)]
 
-    def run_each(tm=None):
-        for e, b in zip(ws, bs):
-            t = tm.start("gemv") if tm else None
-            lin(x, e, b)
-            if tm:
-                tm.stop(t)
+    # One launch per linear straight through the C ABI (preallocated outputs), timed as one batch of
+    # back-to-back launches: the Python wrapper's own time per call is about that of the kernel and would
+    # leave the GPU idle between launches.
+    from selas_amd import _lib
+
+    lib, st, code = _lib.load(), _lib.stream(dev), _lib.code_array(codecs.NF4_CODE)
+    ys = [torch.empty(s, e.shape[0], dtype=torch.bfloat16, device=dev) for e in ws]
+    args = [(x.data_ptr(), s, D, D, e.parts["packed"].data_ptr(), e.parts["absmax"].data_ptr(), 64, code, e.shape[0],
+             b.data_ptr(), y.data_ptr(), e.shape[0], _lib.BF16, None, 0, st) for e, b, y in zip(ws, bs, ys)]
+    f = lib.selas_nf4_linear
+
+    def run_each():
+        for a in args:
+            assert f(*a) == 0
 
     plan = GroupedPlan(tuples, s, dev)
     assert plan.supported
-    for _ in range(warmup):
+    for _ in range(max(2, warmup // 10)):
         run_each()
         nf4_linear_grouped(x, tuples)
         plan.run(x)
     torch.cuda.synchronize(dev)
     tm = Timer()
-    run_each(tm)
+    reps = 5
+    t = tm.start("gemv")
+    for _ in range(reps):
+        run_each()
+    tm.stop(t)
+    # the 38 double-block weights (18432 x 3072, 31.9 MB of NF4 each) alone, back to back
+    t = tm.start("gemv_18432")
+    for _ in range(reps):
+        for a in args[:38]:
+            f(*a)
+    tm.stop(t)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(ys[0], lin(x, ws[0], bs[0]))
     for _ in range(max(3, steps // 2)):
         t = tm.start("grouped_call")
         nf4_linear_grouped(x, tuples)
         tm.stop(t)
-    torch.cuda.synchronize(dev)
+    sustain(lambda: plan.run(x), dev)
     for _ in range(max(5, steps)):
         t = tm.start("grouped_kernel")
         plan.run(x)
         tm.stop(t)
     torch.cuda.synchronize(dev)
-    per = tm.median_ms("gemv")
+    per = tm.mean_ms("gemv") / (reps * len(args))
+    per18 = tm.mean_ms("gemv_18432") / (reps * 38)
+    b18 = ws[0].nbytes + 6 * D * 2 + s * D * 2 + s * 6 * D * 2
     grp = tm.median_ms("grouped_kernel")
     call = tm.median_ms("grouped_call")
+    assert all(torch.equal(a, b) for a, b in zip(plan.outs, ys))
     return {"launches": 76, "bytes": nbytes, "flops": flops, "grouped_kernel_ms": grp,
             "gbs_grouped": nbytes / grp / 1e6, "frac_hbm_grouped": nbytes / grp / 1e6 / PEAK_HBM_GBS,
-            "grouped_call_ms": call, "per_linear_kernel_ms_mean": per, "gbs_per_linear": nbytes / (per * 76) / 1e6}
+            "grouped_call_ms": call, "per_linear_kernel_ms_mean": per, "gbs_per_linear": nbytes / (per * 76) / 1e6,
+            "one_18432x3072": {"kernel_ms_mean": per18, "bytes": b18, "gbs": b18 / per18 / 1e6,
+                               "frac_hbm": b18 / per18 / 1e6 / PEAK_HBM_GBS}}
 
 
 def bench_int8_row(dev, steps, warmup, copies=8):
@@ -334,7 +359,7 @@ def bench_int8_row(dev, steps, warmup, copies=8):
     lib, st = _lib.load(), _lib.stream(dev)
     ys = [torch.empty(s, e.shape[0], dtype=torch.bfloat16, device=dev) for e in ws]
     args = [(x.data_ptr(), s, D, D, e.parts["q"].data_ptr(), e.parts["scale"].data_ptr(), e.shape[0], b.data_ptr(),
-             y.data_ptr(), e.shape[0], _lib.BF16, st) for e, b, y in zip(ws, bs, ys)]
+             y.data_ptr(), e.shape[0], _lib.BF16, None, 0, st) for e, b, y in zip(ws, bs, ys)]
     f = lib.selas_int8_row_linear
     for _ in range(max(2, warmup // 10)):
         for a in args:

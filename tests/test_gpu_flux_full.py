@@ -245,3 +245,65 @@ def test_runner_against_the_oracle_runner():
     assert rel(x, ox) <= L2_REL
     with pytest.raises(FloatingPointError):
         F.euler_update(x, sig, 2, v * float("inf"))
+
+
+def test_full_width_runner_against_the_oracle_runner():
+    # FLUX-dev width (hidden 3072, 24 heads x 128, mlp 12288, context 4096, vec 768) with two double and
+    # two single blocks, batch 1 at 1024^2 (512 text + 4096 image tokens): the runner's prepare and two
+    # steps with Euler updates against the oracle's prepare / step / euler. This runs at real width what
+    # the per-block tests leave out: img_in, the chained gated_add_mod between blocks of one kind, the
+    # double -> single hand-off (cat(txt, img)), final_layer and the sampler update.
+    # Two oracles on the same decoded NF4 operands: the reference's bf16 arithmetic, and exact fp32 math.
+    # After four blocks the bf16 roundings (each GEMM output, each attention probability) add up to a few
+    # 1e-3 of the velocity, whichever order the sums take, so the bound is stated against the exact math:
+    # the GPU's distance from it is at most 1.25x the reference bf16 path's own distance, and the GPU
+    # stays within 1e-2 of the reference bf16 path.
+    model = F.RandomFlux(CFG, "cuda", BF16, seed=11, n_double=2, n_single=2)
+    run = F.FluxRunner(model)
+    dev = torch.device("cuda")
+    g = seeded(48)
+    lt, grid = 512, 64
+    sig = F.get_schedule(28, grid * grid)
+    pooled = torch.randn(1, CFG.vec_dim, generator=g)
+    txt = torch.randn(1, lt, CFG.context_dim, generator=g) * 0.5
+    lat = torch.randn(1, grid * grid, 64, generator=g)
+    cond = run.prepare(sig, 3.5, pooled, txt, F.image_ids(grid, grid), F.text_ids(lt))
+    ocfg = OF.FluxConfig(depth_double=2, depth_single=2)
+    og = oracle_unit(model.globals)
+    mods = [oracle_unit(u) for u in model.mods]
+    doubles = [oracle_unit(u) for u in model.doubles]
+    singles = [oracle_unit(u) for u in model.singles]
+
+    def f32(u):
+        return OF.OracleUnit(u.t, torch.float32)  # the same operand values, fp32 activations
+
+    def oracle_cond(dt, gu, mu):
+        sv = OF.svec(gu, ocfg, sig, 3.5, pooled, dt)
+        omods = OF.modulations(mu, [sv], 2)[0]
+        return sv, OF.prepare(gu, ocfg, sig, 3.5, pooled, txt, F.image_ids(grid, grid), torch.zeros(lt, 3), omods, dt)
+
+    sv, ocond = oracle_cond(BF16, og, mods)
+    _, ocond32 = oracle_cond(torch.float32, f32(og), [f32(u) for u in mods])
+    assert rel(run.svec(sig, 3.5, pooled), sv) < L2_REL
+    for j, n in enumerate(run.main):
+        assert rel(cond.mods[n], ocond.mods[j]) < L2_REL, n
+    assert rel(cond.final_mod, ocond.final_mod) < L2_REL and rel(cond.txt, ocond.txt) < L2_REL
+    x, ox = lat.to(dev), lat
+    for s in (0, 1):
+        print(f"full-width runner step {s}: GPU step", flush=True)
+        v, _ = run.step(s, x, cond)
+        assert v.shape == (1, grid * grid, 64)
+        print(f"full-width runner step {s}: oracle steps on the CPU (bf16, fp32)", flush=True)
+        ov = OF.step(og, doubles, singles, ocfg, s, ox, ocond, BF16)
+        ov32 = OF.step(f32(og), [f32(u) for u in doubles], [f32(u) for u in singles], ocfg, s, ox, ocond32,
+                       torch.float32)
+        gpu_exact, ref_exact, gpu_ref = rel(v, ov32), rel(ov, ov32), rel(v, ov)
+        print(f"full-width runner step {s}: velocity rel L2 GPU-exact {gpu_exact:.2e}, reference bf16-exact "
+              f"{ref_exact:.2e}, GPU-reference bf16 {gpu_ref:.2e}", flush=True)
+        assert gpu_exact <= 1.25 * ref_exact and gpu_ref <= 1e-2
+        x, ox = F.euler_update(x, sig, s, v), OF.euler(ox, sig, s, ov)
+        e = rel(x - lat.to(dev), ox - lat)  # the update itself, not the latents it is added to
+        print(f"full-width runner step {s}: latent update rel L2 {e:.2e}", flush=True)
+        assert e <= 1e-2
+    del model
+    torch.cuda.empty_cache()

@@ -191,3 +191,34 @@ def test_unit_flops_matches_the_published_totals():
     assert OF.unit_flops("double", cfg, 4096, 512, 1)[0] == 2 * 4608 * 113_246_208
     assert OF.unit_flops("single", cfg, 4096, 512, 3)[0] == 3 * 2 * 4608 * 113_246_208
     assert OF.unit_flops("globals", cfg, 4096, 512, 1) == (0.0, 0.0)
+
+
+def test_product_runner_helpers_match_reference_vectors():
+    # selas_amd.flux's own schedule, position ids, timestep embedding and RoPE tables (the values its GPU
+    # runner is fed) against what selas's sampling.py / flux.py produced for the tiny runner: 3 steps over
+    # 16 image tokens, a 4 x 4 latent grid (64 x 64 pixels in selas's image_ids), 8 text tokens.
+    import math
+
+    from selas_amd import flux as PF
+
+    cfg, t, _ = _runner()
+    sig = PF.get_schedule(len(t["in.sigmas"]) - 1, 16)
+    assert torch.equal(torch.tensor(sig, dtype=torch.float64), t["in.sigmas"])
+    img_ids, txt_ids = PF.image_ids(4, 4), PF.text_ids(8)
+    assert torch.equal(img_ids, t["in.img_ids"]) and torch.equal(txt_ids, t["in.txt_ids"])
+    temb = PF.timestep_embedding(torch.tensor(sig[:-1], dtype=torch.float32), 256)
+    assert torch.allclose(temb, t["out.temb"], atol=1e-6, rtol=0)
+    cos, sin = PF.rope_tables(torch.cat((txt_ids, img_ids)), cfg.axes_dim, cfg.theta)
+    assert torch.equal(cos, t["out.cos"]) and torch.equal(sin, t["out.sin"])
+    # The shift at FLUX's own sizes, from its closed form: mu = 0.5 + 0.65 (L - 256) / 3840, so L = 4096
+    # (1024^2) gives mu = 1.15 and sigma(t) = e^mu / (e^mu + 1/t - 1); L = 1024 (512^2) mu = 0.63.
+    for seq, mu in ((4096, 1.15), (1024, 0.5 + 0.65 * 768 / 3840)):
+        s = PF.get_schedule(28, seq)
+        assert s[0] == 1.0 and s[-1] == 0.0 and len(s) == 29
+        for i in (7, 14, 21):
+            tt = 1 - i / 28
+            assert abs(s[i] - math.exp(mu) / (math.exp(mu) + 1 / tt - 1)) < 1e-12
+    assert PF.get_schedule(4, 4096, shift=False) == [1.0, 0.75, 0.5, 0.25, 0.0]
+    # rows are (0, row, col): the last image token of a 64 x 48 grid sits at row 63, column 47
+    ids = PF.image_ids(64, 48)
+    assert ids.shape == (3072, 3) and ids[-1].tolist() == [0.0, 63.0, 47.0] and ids[48].tolist() == [0.0, 1.0, 0.0]

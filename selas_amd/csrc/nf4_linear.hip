@@ -405,11 +405,9 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, c = lane & 31;
 
-  // fp16 codebook, staged in the reduction area.
+  // fp16 codebook, staged in the reduction area until the table is built.
   uint32_t *code16 = reinterpret_cast<uint32_t *>(red);
-  unsigned *rowmax = reinterpret_cast<unsigned *>(red) + 64;
   if (tid < 16) code16[tid] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(code.v[tid]));
-  if (tid < 32) rowmax[tid] = 0u;
   if (wave == 0) {
     // prefix[g] = units (32-row slabs) before weight g: a wave-wide scan, 64 weights at a time.
     int carry = 0;
@@ -427,37 +425,21 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     }
     if (lane == 0) prefix[0] = 0;
   }
-  __syncthreads();
-  {
-    // Entry (b, j) at b*256 + 4*j: fp16 pair (code[b >> 4], code[b & 15]), one replica per lane j.
-    constexpr int kParts = kThreads / 256, kPer = 64 / kParts;
-    const int b = tid & 255, part = tid >> 8;
-    const uint32_t e = code16[b >> 4] | (code16[b & 15] << 16);
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int r = kPer * part + ((j + lane) & (kPer - 1));
-      *reinterpret_cast<uint32_t *>(lds + b * 256 + r * 4) = e;
-    }
-  }
-
-  // x fragments of this wave's slice: block b, sub-step s covers k = 64*(kb0+b) + 32h + 8s .. +8.
+  // This wave's slice of x, block b, sub-step s: k = 64*(kb0+b) + 32h + 8s .. +8 of row c (rows past M
+  // repeat row M-1), loaded once by buffer loads (they cannot touch LDS, so LDS work below need not wait
+  // for them) and in flight during the scan, the first unit's DMA and the table build.
   const int kb0 = wave * BPW;
-  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 64 * kb0 + 32 * h;
-  // Row maxima of |x| (as bf16 magnitude bits: ordered like the values, NaN above Inf).
+  uint4 xraw[BPW][4];
   {
-    uint32_t mx = 0;
+    const auto xrs = make_rsrc(x, static_cast<uint32_t>(((M - 1) * ldx + K) * 2));
+    const uint32_t xoff = (static_cast<uint32_t>(min(c, M - 1)) * static_cast<uint32_t>(ldx) +
+                           static_cast<uint32_t>(64 * kb0 + 32 * h)) * 2u;
 #pragma unroll
     for (int b = 0; b < BPW; ++b)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint4 q = *reinterpret_cast<const uint4 *>(xr + 64 * b + 8 * s);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
-      }
-    __syncthreads();  // rowmax cleared
-    atomicMax(&rowmax[c], mx);
+      for (int s = 0; s < 4; ++s) xraw[b][s] = load_b128(xrs, xoff, static_cast<uint32_t>(64 * b + 8 * s) * 2u);
   }
+  __syncthreads();  // prefix and fp16 codebook ready
 
   uint8_t *stage = lds + L::kStage + wave * L::kCodeBytes;
   // MFMA-order reads: lane (c, h) takes chunk 2b + h of row c.
@@ -465,45 +447,6 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   const int sc_swz = sg_swz<kblocks / 4>(c);
   // v_perm source for table addresses: byte 0 = 4 * lane, byte 1 <- code byte.
   const uint32_t tsel = static_cast<uint32_t>(lane) * 4u;
-
-  __syncthreads();  // table, prefix and row maxima ready
-
-  // The skinny kernel multiplies in fp16: each row of x is scaled by a power of
-  // two that brings its largest magnitude into [2^14, 2^15), which makes the
-  // bf16 -> fp16 conversion exact (8 significant bits into 11; values below
-  // 2^-38 of the row maximum fall into fp16 subnormals or to zero), and the
-  // products with the fp16 codebook accumulate in fp32. The output is scaled
-  // back exactly. Rows whose maximum is 0, Inf or NaN keep scale 1.
-  auto row_scale = [&](int row, bool inverse) {
-    const unsigned e = (rowmax[min(row, M - 1)] >> 7) & 0xffu;  // bf16 exponent field of the row maximum
-    if (e == 0u || e == 0xffu) return 1.0f;
-    const int k = 14 - (static_cast<int>(e) - 127);               // scale = 2^k
-    const int kc = max(-126, min(127, inverse ? -k : k));
-    return __uint_as_float(static_cast<uint32_t>(kc + 127) << 23);
-  };
-  f16x8 xf[BPW][4];
-  {
-    const float sc = row_scale(c, false);
-#pragma unroll
-    for (int b = 0; b < BPW; ++b)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint4 q = *reinterpret_cast<const uint4 *>(xr + 64 * b + 8 * s);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          xf[b][s][2 * i] = static_cast<_Float16>(__uint_as_float(w[i] << 16) * sc);
-          xf[b][s][2 * i + 1] = static_cast<_Float16>(__uint_as_float(w[i] & 0xffff0000u) * sc);
-        }
-      }
-  }
-  // Inverse scales of the output rows this thread finishes (fixed for the launch).
-  float inv_m[L::kOuts];
-#pragma unroll
-  for (int i = 0; i < L::kOuts; ++i) {
-    const int r = wave + NW * i;
-    inv_m[i] = row_scale(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), true);
-  }
 
   const int units_total = prefix[count];
   // Units are dealt out round-robin: workgroup b takes units b, b + G, b + 2G, ... (G = grid size), so
@@ -547,6 +490,64 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
       }
     }
   };
+  // The first unit's codes and scales: their latency overlaps the table build and the x conversion.
+  int g_cur = locate(u_begin, 0);
+  SDesc d_cur = desc(g_cur);
+  int row_cur = (u_begin - prefix[g_cur]) * kSgRows;
+  issue(0, d_cur, row_cur);
+
+  {
+    // Entry (b, j) at b*256 + 4*j: fp16 pair (code[b >> 4], code[b & 15]), one replica per lane j.
+    constexpr int kParts = kThreads / 256, kPer = 64 / kParts;
+    const int b = tid & 255, part = tid >> 8;
+    const uint32_t e = code16[b >> 4] | (code16[b & 15] << 16);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int r = kPer * part + ((j + lane) & (kPer - 1));
+      *reinterpret_cast<uint32_t *>(lds + b * 256 + r * 4) = e;
+    }
+  }
+
+  // The skinny kernel multiplies in fp16: each row of this wave's slice of x is
+  // scaled by a power of two that brings the slice's largest magnitude into
+  // [2^14, 2^15), which makes the bf16 -> fp16 conversion exact (8 significant
+  // bits into 11; values below 2^-38 of that maximum fall into fp16 subnormals
+  // or to zero), and the products with the fp16 codebook accumulate in fp32.
+  // Each wave scales its fp32 partial sums back (exactly: a power of two) before
+  // the waves' partials are added, so no row maximum over all of K is needed.
+  // Rows whose slice maximum is 0, Inf or NaN keep scale 1.
+  f16x8 xf[BPW][4];
+  float inv[16];  // inverse scale of the row each partial-sum register holds
+  {
+    uint32_t mx = 0;  // |x| as bf16 magnitude bits: ordered like the values, NaN above Inf
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t w[4] = {xraw[b][s].x, xraw[b][s].y, xraw[b][s].z, xraw[b][s].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+      }
+    mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), 32)));  // both halves of row c's slice
+    const unsigned e = (mx >> 7) & 0xffu;  // bf16 exponent field of the slice maximum
+    const int k = (e == 0u || e == 0xffu) ? 0 : 14 - (static_cast<int>(e) - 127);  // scale = 2^k
+    const float sc = __uint_as_float(static_cast<uint32_t>(max(-126, min(127, k)) + 127) << 23);
+    const float isc = __uint_as_float(static_cast<uint32_t>(max(-126, min(127, -k)) + 127) << 23);
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t w[4] = {xraw[b][s].x, xraw[b][s].y, xraw[b][s].z, xraw[b][s].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xf[b][s][2 * i] = static_cast<_Float16>(__uint_as_float(w[i] << 16) * sc);
+          xf[b][s][2 * i + 1] = static_cast<_Float16>(__uint_as_float(w[i] & 0xffff0000u) * sc);
+        }
+      }
+    // Register r of a 32x32 result holds row 8*(r/4) + 4h + r%4, whose scale lane (that row) computed.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) inv[r] = __shfl(isc, 8 * (r >> 2) + 4 * h + (r & 3));
+  }
   // Bias and outputs go through buffer resources, not generic pointers: a
   // flat access might touch LDS and would make every later LDS read wait for
   // all outstanding memory operations, the stage DMA included.
@@ -558,7 +559,8 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     return __builtin_amdgcn_raw_buffer_load_b16(rb, static_cast<uint32_t>(n) * 2u, 0, 0);
   };
   // The outputs this thread owns of the unit whose partials are in buffer `buf`:
-  // the NW partials summed in wave order, bias added, rounded to bf16.
+  // the NW partials (each already scaled back) summed in wave order, bias
+  // added, rounded to bf16.
   auto finish = [&](int buf, const SDesc &d, int row0, uint32_t bias_bits) {
     const int N = d.n;
     const float bv = bf16_bits_to_f32(static_cast<uint16_t>(bias_bits));
@@ -580,7 +582,7 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
       const int m = 8 * (r >> 2) + 4 * h + (r & 3);
       const int n = row0 + c;
       if (m < M && n < N)
-        __builtin_amdgcn_raw_buffer_store_b16(bf16_bits_rne(v * inv_m[i] + bv), ry,
+        __builtin_amdgcn_raw_buffer_store_b16(bf16_bits_rne(v + bv), ry,
                                               static_cast<uint32_t>(m * d.ldy + n) * 2u, 0, 0);
     }
   };
@@ -599,14 +601,8 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     }
   };
 
-  // Unit u of the loop: weight g_cur (descriptor d_cur, first row row_cur); the
-  // next unit's weight g_nxt. Unit u-1's outputs are finished during unit u.
-  int g_cur = locate(u_begin, 0);
-  SDesc d_cur = desc(g_cur);
-  int row_cur = (u_begin - prefix[g_cur]) * kSgRows;
-  issue(0, d_cur, row_cur);
   wait_vmcnt<0>();
-  __syncthreads();  // the first unit's codes and scales are in LDS
+  __syncthreads();  // the first unit's codes and scales, and the table, are in LDS
   read_stage(0);
   SDesc d_prev = d_cur;
   int row_prev = row_cur;
@@ -672,12 +668,12 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     if constexpr (L::kRedBufs == 1) {
       __syncthreads();  // every wave has summed unit u-1 from the single buffer
 #pragma unroll
-      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r];
+      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r] * inv[r];
       if (more) read_stage(it + 1);  // its latency overlaps the barrier
       __syncthreads();
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r];
+      for (int r = 0; r < 16; ++r) rw[(wave * 16 + r) * 64 + lane] = acc[r] * inv[r];
       __syncthreads();  // partials of unit u complete; every wave's DMAs of unit u+1 landed
       if (more) read_stage(it + 1);
     }

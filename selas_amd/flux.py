@@ -370,9 +370,11 @@ class RandomFlux:
         return out
 
     @torch.no_grad()
-    def step(self, latents, txt, mods_s, final_mod_s, cos, sin, k: Kernels = FUSED) -> torch.Tensor:
+    def step(self, latents, txt, mods_s, final_mod_s, cos, sin, k: Kernels = FUSED,
+             micro_batch: int | None = None) -> torch.Tensor:
         """Velocity for one step (flux.py:527-582). latents [B, Li, 64] fp32, txt [B, Lt, D] fp32,
-        mods_s: per block [B, kD] for this step, final_mod_s [B, 2D]."""
+        mods_s: per block [B, kD] for this step, final_mod_s [B, 2D]. ``micro_batch``: each block runs
+        the batch in chunks of at most that many images, block by block (flux.py:492-524)."""
         cfg, dt, guard = self.cfg, self.dt, self.dt == torch.float16
         # The blocks use their modulation vectors in fp32 (each block converts its own, flux.py:302, 327):
         # one conversion of all of them is exact and saves a small kernel per block.
@@ -383,18 +385,38 @@ class RandomFlux:
         # Between blocks of one kind, the closing residual add and the next block's mod_in run as one
         # pass (gated_add_mod); the bits are those of the two kernels (same fp32 residual, same statistics).
         chain = CHAIN_BLOCKS and isinstance(k, Kernels)
+        b = latents.shape[0]
+        mb = micro_batch or b
+        chunks = [(a, min(b, a + mb)) for a in range(0, b, mb)]
         h = None
         for i, w in enumerate(self.doubles):
             nxt = mods_s[i + 1] if chain and i + 1 < nd else None
-            r = double_block(w, img, txt, mods_s[i], cos, sin, cfg, dt, guard, k, h, nxt)
-            img, txt, h = r if nxt is not None else (*r, None)
+            if len(chunks) == 1:
+                r = double_block(w, img, txt, mods_s[i], cos, sin, cfg, dt, guard, k, h, nxt)
+                img, txt, h = r if nxt is not None else (*r, None)
+                continue
+            outs = [double_block(w, img[a:e], txt[a:e], mods_s[i][a:e], cos, sin, cfg, dt, guard, k,
+                                 None if h is None else (h[0][a:e], h[1][a:e]),
+                                 None if nxt is None else nxt[a:e]) for a, e in chunks]
+            img, txt = torch.cat([o[0] for o in outs]), torch.cat([o[1] for o in outs])
+            h = (torch.cat([o[2][0] for o in outs]), torch.cat([o[2][1] for o in outs])) if nxt is not None else None
+            del outs
         x = torch.cat((txt, img), dim=1)
         del txt, img
         h = None
         for j, w in enumerate(self.singles):
             nxt = mods_s[nd + j + 1] if chain and j + 1 < ns else None
-            r = single_block(w, x, mods_s[nd + j], cos, sin, cfg, dt, guard, k, h, nxt)
-            x, h = r if nxt is not None else (r, None)
+            if len(chunks) == 1:
+                r = single_block(w, x, mods_s[nd + j], cos, sin, cfg, dt, guard, k, h, nxt)
+                x, h = r if nxt is not None else (r, None)
+                continue
+            outs = [single_block(w, x[a:e], mods_s[nd + j][a:e], cos, sin, cfg, dt, guard, k,
+                                 None if h is None else h[a:e], None if nxt is None else nxt[a:e]) for a, e in chunks]
+            if nxt is not None:
+                x, h = torch.cat([o[0] for o in outs]), torch.cat([o[1] for o in outs])
+            else:
+                x, h = torch.cat(outs), None
+            del outs
         return final_layer(self.globals, x[:, lt:], final_mod_s, dt, k)
 
 
@@ -469,11 +491,17 @@ class StepInfo:
 class FluxRunner:
     """The reference runner's prologue and step (flux.py:392-582) over a model whose units are resident
     on one GPU (``RandomFlux``): no weight streaming, every modulation linear of an image in one grouped
-    launch. Block names follow the reference ("double.i", "single.j")."""
+    launch. Block names follow the reference ("double.i", "single.j"). ``micro_batch`` runs each block
+    over the batch in chunks of at most that many images (the reference's block-major micro-batching,
+    flux.py:492-524): peak activation memory follows the chunk, and every image gets the bits of the
+    unchunked step except in the tiles of a tiled linear that the batch's size makes it split over K."""
 
-    def __init__(self, model: RandomFlux, kernels: Kernels = FUSED):
+    def __init__(self, model: RandomFlux, kernels: Kernels = FUSED, micro_batch: int | None = None):
+        if micro_batch is not None and micro_batch < 1:
+            raise ValueError(f"micro_batch must be a positive image count, got {micro_batch}")
         self.model = model
         self.k = kernels
+        self.micro_batch = micro_batch
         self.cfg = model.cfg
         self.dt = model.dt
         self.guard = model.dt == torch.float16
@@ -523,7 +551,8 @@ class FluxRunner:
         if cache is not None and getattr(cache, "active", False):
             raise NotImplementedError("the step cache is not supported by selas_amd's runner")
         mods_s = [cond.mods[n][s] for n in self.main]
-        out = self.model.step(latents, cond.txt, mods_s, cond.final_mod[s], cond.cos, cond.sin, self.k)
+        out = self.model.step(latents, cond.txt, mods_s, cond.final_mod[s], cond.cos, cond.sin, self.k,
+                              self.micro_batch)
         return out, StepInfo()
 
     @torch.no_grad()

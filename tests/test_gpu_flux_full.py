@@ -307,3 +307,26 @@ def test_full_width_runner_against_the_oracle_runner():
         assert e <= 1e-2
     del model
     torch.cuda.empty_cache()
+
+
+def test_runner_micro_batches_block_by_block():
+    # FluxRunner(micro_batch=m) runs each block over chunks of at most m images (flux.py:492-524). Every
+    # kernel works per token or per (image, head), and these shapes launch no split tiles, so the
+    # velocity has the bits of the unchunked step for chunks of 2 (3 images: 2 + 1) and of 1.
+    cfg = F.FluxConfig(hidden=256, heads=2, mlp_hidden=1024, depth_double=2, depth_single=3, in_channels=64,
+                       context_dim=128, vec_dim=64, axes_dim=(16, 56, 56))
+    model = F.RandomFlux(cfg, "cuda", BF16, seed=9)
+    g = seeded(49)
+    b, lt, grid = 3, 64, 8
+    sig = F.get_schedule(4, grid * grid)
+    pooled = torch.randn(b, cfg.vec_dim, generator=g)
+    txt = torch.randn(b, lt, cfg.context_dim, generator=g)
+    lat = torch.randn(b, grid * grid, 64, generator=g).cuda()
+    whole = F.FluxRunner(model)
+    cond = whole.prepare(sig, 4.0, pooled, txt, F.image_ids(grid, grid), F.text_ids(lt))
+    v, _ = whole.step(1, lat, cond)
+    for mb in (2, 1):
+        vm, _ = F.FluxRunner(model, micro_batch=mb).step(1, lat, cond)
+        assert torch.equal(vm, v), mb
+    with pytest.raises(ValueError):
+        F.FluxRunner(model, micro_batch=0)

@@ -68,19 +68,26 @@ __device__ __forceinline__ void store4(void *p, int64_t i, float4 v) {
 
 // LayerNorm (no affine, eps 1e-6) of a row held as float4 groups v[0..n) at
 // columns 4*(tid + 256*j), then (. * (1 + scale) + shift) stored as OUT.
-template <int OUT>
+// CNV > 0: the row is exactly CNV groups per thread (D = 1024 * CNV), known at
+// compile time (the same sums in the same order, without the bounds tests).
+template <int OUT, int CNV>
 __device__ __forceinline__ void ln_modulate_store(float4 (&v)[kMaxVec], int nvec, int D, const float *shift,
                                                   const float *scale, void *out, int64_t out_row, float *scratch) {
   const int tid = threadIdx.x;
+  if constexpr (CNV > 0) {
+    nvec = CNV;
+    D = 4 * kRowThreads * CNV;
+  }
+  auto in_row = [&](int j) { return CNV > 0 ? j < CNV : (j < nvec && 4 * (tid + kRowThreads * j) < D); };
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < kMaxVec; ++j)
-    if (j < nvec && 4 * (tid + kRowThreads * j) < D) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    if (in_row(j)) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   const float mean = block_sum(s, scratch) / static_cast<float>(D);
   float q = 0.0f;
 #pragma unroll
   for (int j = 0; j < kMaxVec; ++j)
-    if (j < nvec && 4 * (tid + kRowThreads * j) < D) {
+    if (in_row(j)) {
       const float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
       q += (a * a + b * b) + (c * c + d * d);
     }
@@ -89,7 +96,7 @@ __device__ __forceinline__ void ln_modulate_store(float4 (&v)[kMaxVec], int nvec
 #pragma unroll
   for (int j = 0; j < kMaxVec; ++j) {
     const int d = 4 * (tid + kRowThreads * j);
-    if (j < nvec && d < D) {
+    if (in_row(j)) {
       const float4 sc = *reinterpret_cast<const float4 *>(scale + d);
       const float4 sh = *reinterpret_cast<const float4 *>(shift + d);
       float4 o;
@@ -104,7 +111,7 @@ __device__ __forceinline__ void ln_modulate_store(float4 (&v)[kMaxVec], int nvec
 
 // ------------------------------------------------------------------ mod_in
 
-template <int OUT>
+template <int OUT, int CNV>
 __global__ __launch_bounds__(kRowThreads) void mod_in_kernel(const float *__restrict__ x, int L, int D, int64_t x_sb,
                                                              int64_t x_sl, const float *__restrict__ shift,
                                                              const float *__restrict__ scale, int64_t mod_sb,
@@ -113,20 +120,20 @@ __global__ __launch_bounds__(kRowThreads) void mod_in_kernel(const float *__rest
   const int row = blockIdx.x;
   const int b = row / L, l = row - b * L;
   const float *xr = x + b * x_sb + l * x_sl;
-  const int nvec = (D + 4 * kRowThreads - 1) / (4 * kRowThreads);
+  const int nvec = CNV > 0 ? CNV : (D + 4 * kRowThreads - 1) / (4 * kRowThreads);
   float4 v[kMaxVec];
 #pragma unroll
   for (int j = 0; j < kMaxVec; ++j) {
     const int d = 4 * (threadIdx.x + kRowThreads * j);
-    v[j] = (j < nvec && d < D) ? *reinterpret_cast<const float4 *>(xr + d) : make_float4(0, 0, 0, 0);
+    v[j] = (CNV > 0 ? j < CNV : (j < nvec && d < D)) ? *reinterpret_cast<const float4 *>(xr + d) : make_float4(0, 0, 0, 0);
   }
-  ln_modulate_store<OUT>(v, nvec, D, shift + b * mod_sb, scale + b * mod_sb, out, static_cast<int64_t>(row) * D,
+  ln_modulate_store<OUT, CNV>(v, nvec, D, shift + b * mod_sb, scale + b * mod_sb, out, static_cast<int64_t>(row) * D,
                          scratch);
 }
 
 // ------------------------------------------------------------------ gated_add (+ mod_in)
 
-template <int YT, bool MOD, int OUT>
+template <int YT, bool MOD, int OUT, int CNV>
 __global__ __launch_bounds__(kRowThreads) void gated_add_kernel(
     const float *__restrict__ x, int L, int D, int64_t x_sb, int64_t x_sl, const float *__restrict__ g, int64_t g_sb,
     const void *__restrict__ y, int64_t y_sb, int64_t y_sl, int guard, const float *__restrict__ shift,
@@ -137,12 +144,13 @@ __global__ __launch_bounds__(kRowThreads) void gated_add_kernel(
   const float *xr = x + b * x_sb + l * x_sl;
   const float *gr = g + b * g_sb;
   const int64_t yoff = b * y_sb + l * y_sl;
-  const int nvec = (D + 4 * kRowThreads - 1) / (4 * kRowThreads);
+  const int nvec = CNV > 0 ? CNV : (D + 4 * kRowThreads - 1) / (4 * kRowThreads);
+  if constexpr (CNV > 0) D = 4 * kRowThreads * CNV;
   float4 v[kMaxVec];
 #pragma unroll
   for (int j = 0; j < kMaxVec; ++j) {
     const int d = 4 * (threadIdx.x + kRowThreads * j);
-    if (j < nvec && d < D) {
+    if (CNV > 0 ? j < CNV : (j < nvec && d < D)) {
       const float4 xv = *reinterpret_cast<const float4 *>(xr + d);
       const float4 gv = *reinterpret_cast<const float4 *>(gr + d);
       float4 yv = load4<YT>(y, yoff + d);
@@ -157,7 +165,7 @@ __global__ __launch_bounds__(kRowThreads) void gated_add_kernel(
     }
   }
   if constexpr (MOD)
-    ln_modulate_store<OUT>(v, nvec, D, shift + b * mod_sb, scale + b * mod_sb, h, static_cast<int64_t>(row) * D,
+    ln_modulate_store<OUT, CNV>(v, nvec, D, shift + b * mod_sb, scale + b * mod_sb, h, static_cast<int64_t>(row) * D,
                            scratch);
 }
 
@@ -412,11 +420,22 @@ extern "C" int selas_mod_in(const float *x, int64_t B, int64_t L, int64_t D, int
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<uint32_t>(B * L)), blk(kRowThreads);
   const int Li = static_cast<int>(L), Di = static_cast<int>(D);
-  switch (out_dtype) {
-    case SELAS_F32: mod_in_kernel<SELAS_F32><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, shift, scale, mod_sb, out); break;
-    case SELAS_F16: mod_in_kernel<SELAS_F16><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, shift, scale, mod_sb, out); break;
-    default: mod_in_kernel<SELAS_BF16><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, shift, scale, mod_sb, out);
+  // The FLUX width (3072) has its own instantiation: three groups of 4 per thread, no bounds tests.
+#define SELAS_MI(OT, CNV) mod_in_kernel<OT, CNV><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, shift, scale, mod_sb, out)
+  if (D == 3072) {
+    switch (out_dtype) {
+      case SELAS_F32: SELAS_MI(SELAS_F32, 3); break;
+      case SELAS_F16: SELAS_MI(SELAS_F16, 3); break;
+      default: SELAS_MI(SELAS_BF16, 3);
+    }
+  } else {
+    switch (out_dtype) {
+      case SELAS_F32: SELAS_MI(SELAS_F32, 0); break;
+      case SELAS_F16: SELAS_MI(SELAS_F16, 0); break;
+      default: SELAS_MI(SELAS_BF16, 0);
+    }
   }
+#undef SELAS_MI
   return check_launch("mod_in");
 }
 
@@ -436,9 +455,13 @@ int gated_add_impl(const char *what, const float *x, int64_t B, int64_t L, int64
     return set_error(SELAS_EUNSUPPORTED, "%s: rows must be 16-byte aligned", what);
   const dim3 grid(static_cast<uint32_t>(B * L)), blk(kRowThreads);
   const int Li = static_cast<int>(L), Di = static_cast<int>(D);
-#define SELAS_GA(YT, OT)                                                                                          \
-  gated_add_kernel<YT, MOD, OT><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, g, g_sb, y, y_sb, y_sl, guard, shift, \
-                                                    scale, mod_sb, x_out, h)
+#define SELAS_GA(YT, OT)                                                                                              \
+  if (D == 3072)                                                                                                      \
+    gated_add_kernel<YT, MOD, OT, 3><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, g, g_sb, y, y_sb, y_sl, guard, shift, \
+                                                         scale, mod_sb, x_out, h);                                     \
+  else                                                                                                                \
+    gated_add_kernel<YT, MOD, OT, 0><<<grid, blk, 0, s>>>(x, Li, Di, x_sb, x_sl, g, g_sb, y, y_sb, y_sl, guard, shift, \
+                                                         scale, mod_sb, x_out, h)
 #define SELAS_GA_Y(YT)                                  \
   switch (MOD ? h_dtype : SELAS_F32) {                  \
     case SELAS_F32: SELAS_GA(YT, SELAS_F32); break;     \

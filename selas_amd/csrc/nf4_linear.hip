@@ -391,6 +391,67 @@ __device__ __forceinline__ int sg_swz(int r) {
   else return (r >> 2) & 3;
 }
 
+// A wave's slice of x for the streaming skinny kernels, in MFMA order: out[b][s] holds, for lane (c, h),
+// the 8 elements k = 64*(kb0+b) + 32h + 8s .. +8 of row c (rows past M repeat row M-1).
+// Lane (c, h) needs row c, so loads straight into registers in that order touch 32 rows, 32 cache
+// lines, per instruction, and measured slower by 2.2 us per launch. The slice goes through LDS
+// instead: one 64-wide block (32 rows x 128 bytes) per round of 4 DMA instructions, each covering 8
+// whole rows, two rounds in flight in the wave's two 4 KiB buffers at LDS [8192 wave, +8192). Chunk p
+// of row r sits at physical chunk p ^ swz(r), so that the MFMA-order reads are free of bank conflicts.
+// The caller owns LDS [0, 65536) until a barrier after this returns (its code table or stages are
+// built there afterwards), and has no vector memory operation of this wave in flight.
+template <int BPW>
+__device__ __forceinline__ void load_x_slice(const uint16_t *x, int64_t ldx, int M, int K, int kb0, int wave,
+                                             int lane, uint4 (&out)[BPW][4]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int h = lane >> 5, c = lane & 31;
+  uint32_t off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = 64 * j + lane, r = q >> 3, p = (q & 7) ^ sg_swz<8>(r);
+    off[j] = (static_cast<uint32_t>(min(r, M - 1)) * static_cast<uint32_t>(ldx) + static_cast<uint32_t>(64 * kb0)) *
+                 2u + 16u * static_cast<uint32_t>(p);
+  }
+  // The make_rsrc descriptor as four words for the asm operand.
+  const uint64_t xp = reinterpret_cast<uint64_t>(x);
+  const u32x4 desc = {static_cast<uint32_t>(xp), static_cast<uint32_t>(xp >> 32) & 0xffffu,
+                      static_cast<uint32_t>(((M - 1) * ldx + K) * 2), 0x00020000u};
+  const uint32_t base = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wave)) * 8192u;
+  // The DMAs are issued by inline asm, uncounted by the compiler: for a counted LDS DMA it waits for all
+  // of them (the next round's included) before every LDS read. The explicit waits order the reads
+  // instead; any wait of the compiler's own is only made longer by the uncounted ones.
+  auto issue = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :
+                   : "s"(base + static_cast<uint32_t>((b & 1) * 4096 + 1024 * j)), "v"(off[j]), "s"(desc),
+                     "s"(128u * b)
+                   : "memory", "m0");
+  };
+  // Reads by LDS address (this file's skinny kernels declare no static LDS, so dynamic LDS starts at 0).
+  const uint32_t rd = base + static_cast<uint32_t>(c * 128);
+  const int sw = sg_swz<8>(c);
+  issue(0);
+  if constexpr (BPW > 1) issue(1);
+#pragma unroll
+  for (int b = 0; b < BPW; ++b) {
+    if (b + 1 < BPW) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // round b landed, round b+1 may not
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t a = rd + static_cast<uint32_t>((b & 1) * 4096 + 16 * ((4 * h + s) ^ sw));
+      out[b][s] = __builtin_bit_cast(
+          uint4, *reinterpret_cast<const __attribute__((address_space(3))) u32x4 *>(static_cast<uintptr_t>(a)));
+    }
+    if (b + 2 < BPW) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the buffer's reads are done before it is refilled
+      issue(b + 2);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
 template <int NW, int BPW>
 __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     const uint16_t *__restrict__ x, int64_t ldx, int M, const GemvDesc *__restrict__ descs, int count,
@@ -425,20 +486,12 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
     }
     if (lane == 0) prefix[0] = 0;
   }
-  // This wave's slice of x, block b, sub-step s: k = 64*(kb0+b) + 32h + 8s .. +8 of row c (rows past M
-  // repeat row M-1), loaded once by buffer loads (they cannot touch LDS, so LDS work below need not wait
-  // for them) and in flight during the scan, the first unit's DMA and the table build.
+  // This wave's slice of x (block b, sub-step s: k = 64*(kb0+b) + 32h + 8s .. +8 of row c), staged
+  // through the table area before the table is built.
   const int kb0 = wave * BPW;
   uint4 xraw[BPW][4];
-  {
-    const auto xrs = make_rsrc(x, static_cast<uint32_t>(((M - 1) * ldx + K) * 2));
-    const uint32_t xoff = (static_cast<uint32_t>(min(c, M - 1)) * static_cast<uint32_t>(ldx) +
-                           static_cast<uint32_t>(64 * kb0 + 32 * h)) * 2u;
-#pragma unroll
-    for (int b = 0; b < BPW; ++b)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xraw[b][s] = load_b128(xrs, xoff, static_cast<uint32_t>(64 * b + 8 * s) * 2u);
-  }
+  static_assert(8 * 8192 <= kSgTableBytes, "x staging fits the table area");
+  load_x_slice<BPW>(x, ldx, M, K, kb0, wave, lane, xraw);
   __syncthreads();  // prefix and fp16 codebook ready
 
   uint8_t *stage = lds + L::kStage + wave * L::kCodeBytes;
@@ -747,14 +800,19 @@ __global__ __launch_bounds__(64 * NW, 1) void int8_gemv_stream(
   }
 
   // x fragments of this wave's slice (block b, sub-step s: k = 64*(kb0+b) + 32h + 8s .. +8; rows
-  // past M repeat row M-1) and the slice's sum_k x per row, against ones.
+  // past M repeat row M-1), staged through the stage and reduction areas before the first unit's DMA,
+  // and the slice's sum_k x per row, against ones.
   const int kb0 = wave * BPW;
-  const uint16_t *xr = x + static_cast<int64_t>(min(c, M - 1)) * ldx + 64 * kb0 + 32 * h;
+  static_assert(8 * 8192 <= L::kPrefix, "x staging fits below the prefix area");
   bf16x8 xf[BPW][4];
+  {
+    uint4 xraw[BPW][4];
+    load_x_slice<BPW>(x, ldx, M, 64 * kblocks, kb0, wave, lane, xraw);
 #pragma unroll
-  for (int b = 0; b < BPW; ++b)
+    for (int b = 0; b < BPW; ++b)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) xf[b][s] = *reinterpret_cast<const bf16x8 *>(xr + 64 * b + 8 * s);
+      for (int s = 0; s < 4; ++s) xf[b][s] = __builtin_bit_cast(bf16x8, xraw[b][s]);
+  }
   const uint32_t one2 = 0x3F803F80u;
   const bf16x8 ones = __builtin_bit_cast(bf16x8, make_uint4(one2, one2, one2, one2));
   f32x16 accx = f32x16{};
@@ -2040,6 +2098,8 @@ extern "C" int selas_nf4_linear_grouped(const void *x, int64_t M, int64_t K, int
                                          "at most %d weights", kSgMaxDescs);
   if (!aligned(x, 16) || ldx % 8 || !aligned(descs, 8))
     return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: x rows must be 16-byte aligned");
+  if (((M - 1) * ldx + K) * 2 >= (1ll << 32))
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped: x spans 4 GiB or more");
   if (total_n <= 0 || total_n >= (1ll << 36))
     return set_error(SELAS_EINVAL, "nf4_linear_grouped: total_n must be the sum of the weights' row counts");
   if (total_n * (K / 2) >= (1ll << 32))
@@ -2067,6 +2127,8 @@ extern "C" int selas_int8_row_linear_grouped(const void *x, int64_t M, int64_t K
                                          "at most %d weights", kSgMaxDescs);
   if (!aligned(x, 16) || ldx % 8 || !aligned(descs, 8))
     return set_error(SELAS_EUNSUPPORTED, "int8_row_linear_grouped: x rows must be 16-byte aligned");
+  if (((M - 1) * ldx + K) * 2 >= (1ll << 32))
+    return set_error(SELAS_EUNSUPPORTED, "int8_row_linear_grouped: x spans 4 GiB or more");
   if (total_n <= 0 || total_n >= (1ll << 36))
     return set_error(SELAS_EINVAL, "int8_row_linear_grouped: total_n must be the sum of the weights' row counts");
   if (total_n * K >= (1ll << 32))
@@ -2174,6 +2236,8 @@ extern "C" int selas_nf4_linear_grouped_static(const void *x, int64_t M, int64_t
                      "nf4_linear_grouped_static: needs blocksize 64, K = 1024, 2048 or 3072 and M <= 32");
   if (!aligned(x, 16) || ldx % 8)
     return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: x rows must be 16-byte aligned");
+  if (((M - 1) * ldx + K) * 2 >= (1ll << 32))
+    return set_error(SELAS_EUNSUPPORTED, "nf4_linear_grouped_static: x spans 4 GiB or more");
   int64_t total_n = 0;
   for (int64_t i = 0; i < count; ++i) {
     const selas_nf4_gemv_desc &d = descs[i];

@@ -572,15 +572,19 @@ __global__ __launch_bounds__(64 * NW, 1) void nf4_gemv_stream(
   f16x8 xf[BPW][4];
   float inv[16];  // inverse scale of the row each partial-sum register holds
   {
-    uint32_t mx = 0;  // |x| as bf16 magnitude bits: ordered like the values, NaN above Inf
+    // |x| as bf16 magnitude bits, ordered like the values (NaN above Inf): a running maximum per 16-bit
+    // half (one mask and one packed max per word), the two halves combined at the end.
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 mx2 = {0, 0};
 #pragma unroll
     for (int b = 0; b < BPW; ++b)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const uint32_t w[4] = {xraw[b][s].x, xraw[b][s].y, xraw[b][s].z, xraw[b][s].w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+        for (int i = 0; i < 4; ++i) mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
       }
+    uint32_t mx = max(static_cast<uint32_t>(mx2.x), static_cast<uint32_t>(mx2.y));
     mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), 32)));  // both halves of row c's slice
     const unsigned e = (mx >> 7) & 0xffu;  // bf16 exponent field of the slice maximum
     const int k = (e == 0u || e == 0xffu) ? 0 : 14 - (static_cast<int>(e) - 127);  // scale = 2^k

@@ -240,8 +240,8 @@ typedef struct selas_nf4_gemv_desc {
 
 /*
  * `count` quantized linears that share one input x [M, K] (M <= 32, K = 1024,
- * 2048 or 3072, blocksize 64, bf16, at most 1023 weights, 16-byte aligned codes),
- * computed by one launch: y_i = x W_i^T + b_i.
+ * 2048 or 3072, blocksize 64, bf16, at most 1023 weights, 16-byte aligned codes
+ * and x rows, x spanning under 4 GiB), computed by one launch: y_i = x W_i^T + b_i.
  * `descs` is a device array of `count` descriptors and total_n the sum of
  * their n (it sizes the launch). Each output has the bits selas_nf4_linear
  * gives for that weight alone.
@@ -283,7 +283,8 @@ int selas_nf4_linear_grouped_static(const void *x, int64_t M, int64_t K, int64_t
 
 /*
  * selas_nf4_linear_grouped for int8_row weights (M <= 32, K = 1024, 2048 or
- * 3072, bf16): in each descriptor `packed` holds q [n, K] (16-byte aligned) and
+ * 3072, bf16, 16-byte aligned x rows, x spanning under 4 GiB): in each
+ * descriptor `packed` holds q [n, K] (16-byte aligned) and
  * `absmax` the n row scales. Each output has the bits selas_int8_row_linear
  * gives for that weight alone (the same kernel serves M <= 32 there).
  * Replaces the per-weight UnitView.linear calls of FluxRunner.modulations

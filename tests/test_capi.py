@@ -157,6 +157,22 @@ def test_split_launch_without_its_workspace_is_refused_before_any_device_call():
             _lib.call("selas_nf4_linear_batched", ctypes.addressof(arr), 1, 64, _code(), _lib.BF16, ws, nbytes, None)
 
 
+def test_grouped_skinny_refuses_an_x_of_4_gib_before_any_device_call():
+    # The streaming kernels address x through a 32-bit buffer range: (M - 1) * ldx + K elements must stay
+    # under 4 GiB. 32 rows at a row stride of 2^27 elements span 8.3 GB.
+    x = ctypes.c_void_p(1 << 20)
+    descs = (_lib.GemvDesc * 1)()
+    descs[0] = _lib.GemvDesc(x.value, x.value, None, x.value, 96, 96)
+    m, k, ldx = 32, 3072, 1 << 27
+    with pytest.raises(_lib.Unsupported, match="4 GiB"):
+        _lib.call("selas_nf4_linear_grouped", x, m, k, ldx, x, 1, 96, 64, _code(), _lib.BF16, None)
+    with pytest.raises(_lib.Unsupported, match="4 GiB"):
+        _lib.call("selas_int8_row_linear_grouped", x, m, k, ldx, x, 1, 96, _lib.BF16, None)
+    with pytest.raises(_lib.Unsupported, match="4 GiB"):
+        _lib.call("selas_nf4_linear_grouped_static", x, m, k, ldx, ctypes.addressof(descs), 1, 64, _code(),
+                  _lib.BF16, None)
+
+
 def test_eager_segments_are_the_reference_math_and_stay_off_the_cpu():
     # The eager fallback of Kernels is the segment math of selas (flux.py:117-147, 164-200); on the CPU it
     # equals the oracle's restatement (same torch ops in the same order: bit for bit), but Kernels itself

@@ -265,6 +265,19 @@ def test_streaming_skinny_other_k(dev, k):
     check_close(int8_row_linear(x, q, s, (n, k), b), oracle_linear(x, w_ref, b))
 
 
+@pytest.mark.parametrize("k", [1024, 2048, 3072])
+def test_streaming_skinny_every_m_with_strided_x(dev, k):
+    # x goes through LDS as in the NF4 kernel: every M from 1 to 32, x a column slice of a wider buffer.
+    n = 160
+    q, s, w_ref = make_weight(n, k, 9 + k, dev)
+    wide = torch.randn(32, k + 192, generator=seeded(k + 5)).to(torch.bfloat16).to(dev)
+    for m in range(1, 33):
+        x = wide[:m, 64:64 + k]
+        y = int8_row_linear(x, q, s, (n, k))
+        check_close(y, oracle_linear(x, w_ref))
+        assert torch.equal(y, int8_row_linear(x.contiguous(), q, s, (n, k)))
+
+
 def test_full_size_single_linear(dev):
     # The 1536-token linear (W 12288 x 3072 ~ N(0, 0.02) seed 0, X 1536 x 3072 seed 1) with int8_row
     # weights: rows sampled against the oracle.

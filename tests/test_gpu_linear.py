@@ -164,6 +164,21 @@ def test_full_size_single_linear(dev):
     assert torch.isfinite(y).all()
 
 
+@pytest.mark.parametrize("k", [1024, 2048, 3072])
+def test_streaming_skinny_every_m_with_strided_x(dev, k):
+    # The streaming kernel copies each wave's slice of x through LDS, 32 rows x 128 bytes per round, rows past M
+    # repeating row M-1. Every M from 1 to 32, with x a column slice of a wider buffer (row stride k + 192).
+    n = 160
+    p, a, w_ref = make_weight(n, k, 7 + k, dev)
+    wide = torch.randn(32, k + 192, generator=seeded(k)).to(torch.bfloat16).to(dev)
+    for m in range(1, 33):
+        x = wide[:m, 64:64 + k]
+        assert x.stride() == (k + 192, 1)
+        y = nf4_linear(x, p, a, 64, codecs.NF4_CODE, (n, k), None)
+        check_close(y, oracle_linear(x, w_ref))
+        assert torch.equal(y, nf4_linear(x.contiguous(), p, a, 64, codecs.NF4_CODE, (n, k), None))
+
+
 def test_grouped_skinny_equals_one_by_one(dev):
     from selas_amd.linear import nf4_linear_grouped
 

@@ -419,15 +419,20 @@ __device__ __forceinline__ void load_x_slice(const uint16_t *x, int64_t ldx, int
   const uint32_t base = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wave)) * 8192u;
   // The DMAs are issued by inline asm, uncounted by the compiler: for a counted LDS DMA it waits for all
   // of them (the next round's included) before every LDS read. The explicit waits order the reads
-  // instead; any wait of the compiler's own is only made longer by the uncounted ones.
+  // instead; any wait of the compiler's own is only made longer by the uncounted ones. M0 (the DMA's
+  // LDS address) is saved and restored around each, since the compiler keeps M0 out of clobber lists;
+  // an SALU write of M0 needs one wait state before an LDS DMA reads it.
   auto issue = [&](int b) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                   :
-                   : "s"(base + static_cast<uint32_t>((b & 1) * 4096 + 1024 * j)), "v"(off[j]), "s"(desc),
-                     "s"(128u * b)
-                   : "memory", "m0");
+    for (int j = 0; j < 4; ++j) {
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+          "s_nop 0\n\ts_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "s"(base + static_cast<uint32_t>((b & 1) * 4096 + 1024 * j)), "v"(off[j]), "s"(desc), "s"(128u * b)
+          : "memory");
+    }
   };
   // Reads by LDS address (this file's skinny kernels declare no static LDS, so dynamic LDS starts at 0).
   const uint32_t rd = base + static_cast<uint32_t>(c * 128);
